@@ -1,0 +1,265 @@
+"""Benchmark of the MI355X MoE expert path (BASELINE.json metric).
+
+Default workload (Qwen3-30B-A3B shape, MoE layer
+forward, bf16): T=8192 tokens, D=2048, H=768, E=128 experts, top-8 softmax
+router with renormalised weights.  One step = router (gate GEMM as upstream
+runs it, then the HIP top-k) -> route (histogram + stable sort) -> permute
+-> grouped GEMM w13 + SwiGLU -> grouped GEMM w2 + score + un-permute ->
+K-way sum, on inputs already resident in HBM.
+
+Prints ONE JSON line (bench contract) with `roofline` for the dominant
+kernel (the w13 grouped GEMM, timed live with HIP events on the stream it
+runs on) and `cpu_baseline` (the CPU oracle on a bounded token sample).
+
+Other configs (--config c1|c3|c4) are for development runs.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "MoE-layer tokens/s + grouped-GEMM TFLOP/s (% MFMA peak), Qwen3-30B-A3B shape"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    "c1": dict(name="C1 Llama4-debugmodel MoE FFN forward", T=2048, D=256, H=512, E=8, K=1, router="sigmoid",
+               norm=False, score_before=True, backward=False),
+    "c2": dict(name="C2 Qwen3-30B-A3B MoE layer forward", T=8192, D=2048, H=768, E=128, K=8, router="softmax",
+               norm=True, score_before=False, backward=False),
+    "c3": dict(name="C3 Llama4-Scout MoE layer forward+backward (routed experts)", T=8192, D=5120, H=8192, E=16,
+               K=1, router="sigmoid", norm=False, score_before=True, backward=True),
+    "c4": dict(name="C4 DeepSeek-V3 expert shard forward (Zipf 1.2)", T=32768, D=7168, H=2048, E=32, K=1,
+               router="zipf", norm=False, score_before=False, backward=False),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=2048, help="token sample for the CPU oracle baseline")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs the MoE expert path on one GPU only; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    ops = importlib.import_module("torchtitan-ascend_amd.ops")
+    F = importlib.import_module("torchtitan-ascend_amd.functional")
+    cfg = CONFIGS[args.config]
+    T, D, H, E, K = cfg["T"], cfg["D"], cfg["H"], cfg["E"], cfg["K"]
+    M = T * K
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    log(f"config {args.config}: T={T} D={D} H={H} E={E} K={K}")
+
+    x = torch.randn(T, D, device=dev).to(torch.bfloat16)
+    w13 = (torch.randn(E, 2 * H, D, device=dev) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(E, D, H, device=dev) * 0.02).to(torch.bfloat16)
+    w_router = (torch.randn(E, D, device=dev) * 0.02).to(torch.bfloat16)
+    zipf_idx = None
+    if cfg["router"] == "zipf":
+        rng = np.random.default_rng(0)
+        r = np.arange(1, 29, dtype=np.float64)
+        w = r ** -1.2
+        c = np.floor(M * w / w.sum()).astype(np.int64)
+        c[0] += M - c.sum()
+        counts = np.zeros(E, np.int64)
+        counts[rng.permutation(E)[:28]] = c
+        lab = rng.permutation(np.repeat(np.arange(E), counts))
+        zipf_idx = torch.from_numpy(lab.reshape(T, K)).to(dev)
+        zipf_scores = torch.rand(T, K, device=dev)
+
+    def router():
+        if zipf_idx is not None:
+            return zipf_scores, zipf_idx
+        logits = torch.matmul(x, w_router.t())  # upstream router gate (nn.Linear, bf16)
+        return ops.router_topk(logits, K, cfg["router"], cfg["norm"])
+
+    def step_forward():
+        scores, idx = router()
+        return F.moe_experts_forward(x, scores, idx, w13, w2, E, cfg["score_before"])
+
+    if cfg["backward"]:
+        w13p = w13.clone().requires_grad_(True)
+        w2p = w2.clone().requires_grad_(True)
+        dout = torch.randn(T, D, device=dev).to(torch.bfloat16)
+        xg = x.clone().requires_grad_(True)
+
+        def step():
+            scores, idx = router()
+            scores = scores.detach().requires_grad_(True)
+            out = F.moe_experts_forward(xg, scores, idx, w13p, w2p, E, cfg["score_before"])
+            out.backward(dout)
+            return out
+    else:
+        def step():
+            with torch.no_grad():
+                return step_forward()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log("warmup done")
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    log(f"timed {args.steps} steps: {ms:.3f} ms/step")
+
+    # ---- per-stage breakdown and the dominant kernel, timed live --------------
+    with torch.no_grad():
+        scores, idx = router()
+        r = ops.route(idx, E, scores.reshape(-1).float())
+        routed = ops.gather_rows(x, r.sorted_indices, K, r.sorted_scores if cfg["score_before"] else None)
+        a, _ = ops.grouped_mm_swiglu(routed, w13, r.offs)
+        scale = None if cfg["score_before"] else r.sorted_scores
+
+        def w2_stage():
+            if K == 1:
+                return ops.grouped_mm_unpermute(a, w2, r.offs, scale, r.sorted_indices, T)
+            return ops.grouped_mm_unpermute(a, w2, r.offs, scale, r.sorted_indices, M)
+
+        ybuf = w2_stage()
+        stages = {
+            "router": lambda: router(),
+            "route": lambda: ops.route(idx, E, scores.reshape(-1).float()),
+            "permute": lambda: ops.gather_rows(x, r.sorted_indices, K,
+                                               r.sorted_scores if cfg["score_before"] else None),
+            "gemm_w13_swiglu": lambda: ops.grouped_mm_swiglu(routed, w13, r.offs),
+            "gemm_w2_unpermute": w2_stage,
+        }
+        if K > 1:
+            stages["sum_topk"] = lambda: ops.sum_topk(ybuf, K)
+        reps = 20
+        stage_us = {}
+        for name, fn in stages.items():
+            fn()
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(reps):
+                fn()
+            e.record()
+            torch.cuda.synchronize()
+            stage_us[name] = s.elapsed_time(e) * 1000.0 / reps
+    log(f"stages (us): {json.dumps({k: round(v, 1) for k, v in stage_us.items()})}")
+
+    w13_flops = 4.0 * M * D * H
+    w2_flops = 2.0 * M * D * H
+    gemm_us = stage_us["gemm_w13_swiglu"] + stage_us["gemm_w2_unpermute"]
+    gemm_tflops = (w13_flops + w2_flops) / (gemm_us * 1e-6) / 1e12
+    w13_tflops = w13_flops / (stage_us["gemm_w13_swiglu"] * 1e-6) / 1e12
+    permute_bytes = T * D * 2 + M * D * 2 + 8 * M
+    permute_gbs = permute_bytes / (stage_us["permute"] * 1e-6) / 1e9
+
+    fwd_flops = 6.0 * M * D * H
+    total_flops = fwd_flops * (3 if cfg["backward"] else 1)
+    tokens_per_s = T / (ms * 1e-3)
+    result = {
+        "metric": METRIC,
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: x~N(0,1), weights~N(0,0.02), random-init router",
+        "config": {"workload": cfg["name"], "tokens": T, "dim": D, "hidden": H, "experts": E, "top_k": K,
+                   "router": cfg["router"], "score_before_experts": cfg["score_before"],
+                   "backward": cfg["backward"]},
+        "layer_tflops": round(total_flops / (ms * 1e-3) / 1e12, 1),
+        "grouped_gemm_tflops": round(gemm_tflops, 1),
+        "grouped_gemm_frac_of_peak": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
+        "permute_gbs": round(permute_gbs, 1),
+        "permute_frac_of_hbm": round(permute_gbs / PEAK_HBM_GBS, 4),
+        "stage_us": {k: round(v, 2) for k, v in stage_us.items()},
+        "roofline": {
+            "kernel": "gg_rows_kernel<EPI_SWIGLU> (grouped GEMM w13 + SwiGLU)",
+            "bound": "mfma",
+            "achieved": round(w13_tflops, 1),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(w13_tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+            "algorithmic_flops_per_launch": w13_flops,
+            "avg_launch_us": round(stage_us["gemm_w13_swiglu"], 2),
+        },
+    }
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args, cfg, x, w13, w2, router)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(args, cfg, x, w13, w2, router):
+    """The CPU oracle (numpy restatement of the reference path) on a token sample."""
+    import numpy as np
+    import torch
+
+    from oracle import moe_oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"), default=1)
+    except Exception:  # pragma: no cover
+        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
+    Ts = min(args.cpu_tokens, cfg["T"])
+    with torch.no_grad():
+        scores, idx = router()
+    xs = x[:Ts].float().cpu().numpy()
+    ss = scores[:Ts].float().cpu().numpy()
+    ix = idx[:Ts].cpu().numpy()
+    w13n = w13.float().cpu().numpy()
+    w2n = w2.float().cpu().numpy()
+    log(f"cpu baseline: oracle on {Ts} tokens, {threads} BLAS threads")
+    t0 = time.perf_counter()
+    O.moe_forward(xs, ss, ix, w13n, w2n, cfg["E"], cfg["score_before"])
+    dt = time.perf_counter() - t0
+    try:
+        model = [ln.split(":", 1)[1].strip() for ln in open("/proc/cpuinfo") if ln.startswith("model name")][0]
+    except Exception:  # pragma: no cover
+        model = "unknown"
+    return {
+        "value": round(Ts / dt, 1),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{Ts} of {cfg['T']} tokens of the same workload (forward), oracle.moe_oracle.moe_forward, "
+                  f"{dt:.2f} s on {model}",
+    }
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,294 @@
+/*
+ * ttamd_moe.h -- C ABI of the MI355X (gfx950) MoE expert path.
+ *
+ * Plain pointers and sizes only; no torch types.  Every pointer named
+ * "device" is HBM memory of the current HIP device; `stream` is a
+ * hipStream_t passed as void* (NULL = the legacy default stream).  All calls
+ * are asynchronous on `stream` and never synchronise the host.
+ *
+ * Return value: 0 on success, otherwise a TTAMD_E* code; the message of the
+ * last failure on the calling thread is returned by ttamd_last_error().
+ * Argument checks (null pointers, sizes, alignment, 32-bit index range) are
+ * done on the host before anything is launched, so a rejected call launches
+ * nothing.
+ *
+ * bf16 tensors are raw 16-bit brain-float bits, row-major.  Routed rows are
+ * numbered j = 0..M-1 with M = num_tokens * topk; "flat" slot s = t*topk + k
+ * is the k-th expert choice of token t (the order of
+ * selected_experts_indices.view(-1) in the reference).
+ *
+ * Group offsets follow torch._grouped_mm as the reference calls it
+ * (torchtitanturbo/models/common/npu_gmm.py:29): `offs` is the INCLUSIVE
+ * cumulative sum of per-expert row counts, int32[E]; expert e owns rows
+ * [offs[e-1], offs[e]) with offs[-1] = 0.  Rows at or past offs[E-1] are not
+ * read and not written.
+ */
+#ifndef TTAMD_MOE_H
+#define TTAMD_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TTAMD_ABI_VERSION 1
+
+enum {
+  TTAMD_OK = 0,
+  TTAMD_EINVAL = 1,  /* bad argument: null pointer, size, alignment, range */
+  TTAMD_ERUNTIME = 2 /* a HIP runtime call failed (launch, attribute query) */
+};
+
+/* Score function applied by the router top-k (upstream TokenChoiceTopKRouter). */
+enum { TTAMD_SCORE_SOFTMAX = 0, TTAMD_SCORE_SIGMOID = 1 };
+
+int ttamd_abi_version(void);
+const char* ttamd_last_error(void);
+
+/* ------------------------------------------------------------------------ *
+ * Routing: router top-k, histogram, stable counting sort, row permute.      *
+ * ------------------------------------------------------------------------ */
+
+/*
+ * Router top-k over per-token expert logits (fp32 [T,E]).
+ * Replaces the selection stage of upstream TokenChoiceTopKRouter; the
+ * in-reference closed form is torchtitanturbo/models/qwen3_5/model.py:757-765
+ * (softmax in fp32, topk, renormalise by the sum of the k values).
+ *   score = softmax(logits) or sigmoid(logits), fp32;
+ *   pick k experts with the largest score (ties: lower expert id first),
+ *   in descending score order;
+ *   if renorm: top_scores /= (sum of the k picked scores + renorm_eps);
+ *   top_scores *= route_scale.
+ * expert_bias (nullable, fp32[E]) is added to the score for SELECTION only
+ * (the returned score is the unbiased one), as upstream's load-balancing
+ * bias does.  Outputs: top_scores fp32[T,K], top_indices int64[T,K].
+ * Requires 1 <= K <= E <= 1024, K <= 16.
+ */
+int ttamd_router_topk(const float* logits, const float* expert_bias,
+                      int64_t num_tokens, int num_experts, int topk,
+                      int score_func, int renorm, float renorm_eps,
+                      float route_scale, float* top_scores,
+                      int64_t* top_indices, void* stream);
+
+/* Bytes of device workspace ttamd_moe_route / ttamd_moe_token_permute need. */
+size_t ttamd_route_workspace_bytes(int64_t num_flat, int num_experts);
+
+/*
+ * Per-expert histogram + stable counting sort of flat expert labels.
+ * Replaces upstream dispatch's `torch.histc(idx.view(-1), bins=E)` +
+ * `torch.argsort(idx.view(-1), stable=True)` (reached from
+ * torchtitanturbo/models/common/npu_gmm.py:106-108) and the index half of
+ * torch_npu.npu_moe_token_permute (npu_permute.py:74-76).
+ *   labels: device int64 (labels_are_int64=1) or int32 [num_flat]
+ *   counts[e]   = #{s : labels[s] == e}                       int32[E]
+ *   offsets[e]  = sum_{e'<e} counts[e'], offsets[E] = #valid   int32[E+1]
+ *   sorted_indices[j] = the j-th flat slot in stable label order int32[M]
+ *   inverse[s]  = position j of slot s (nullable)               int32[M]
+ *   sorted_scores[j] = scores[sorted_indices[j]] (both nullable) fp32[M]
+ * Labels outside [0,E) are sorted after every valid label (positions
+ * [offsets[E], M)), so sorted_indices is always a permutation of [0,M).
+ * Bit-exact: identical to a stable argsort for every valid input.
+ */
+int ttamd_moe_route(const void* labels, int labels_are_int64, int64_t num_flat,
+                    int num_experts, const float* scores, int32_t* counts,
+                    int32_t* offsets, int32_t* sorted_indices,
+                    int32_t* inverse, float* sorted_scores, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/*
+ * Row gather of the permute: out[j] = in[src_index[j] / topk], optionally
+ * multiplied by row_scale[j] in fp32 and rounded to bf16 once (upstream
+ * dispatch with score_before_experts).  bf16 [num_in_rows, hidden] ->
+ * bf16 [num_out_rows, hidden].  hidden % 8 == 0, 16-byte aligned rows.
+ */
+int ttamd_moe_gather_rows(const void* in, const int32_t* src_index,
+                          const float* row_scale, int64_t num_in_rows,
+                          int64_t num_out_rows, int64_t hidden, int topk,
+                          void* out, void* stream);
+
+/*
+ * Drop-in for torch_npu.npu_moe_token_permute(tokens, indices)
+ * (torchtitanturbo/models/common/npu_permute.py:74-76): stable sort of the
+ * flat labels and gather of token rows.  tokens bf16 [T,D]; labels
+ * [T*topk] (int64 or int32); permuted bf16 [T*topk, D];
+ * sorted_indices int32 [T*topk] = stable argsort of the labels (the map
+ * ttamd_moe_token_unpermute takes back).  num_experts bounds the label
+ * range (labels outside [0,num_experts) sort last).  counts (nullable)
+ * int32[num_experts] receives the histogram.
+ */
+int ttamd_moe_token_permute(const void* tokens, const void* labels,
+                            int labels_are_int64, int64_t num_tokens,
+                            int64_t hidden, int topk, int num_experts,
+                            void* permuted, int32_t* sorted_indices,
+                            int32_t* counts, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* Bytes of device workspace ttamd_moe_token_unpermute needs. */
+size_t ttamd_unpermute_workspace_bytes(int64_t num_tokens, int topk);
+
+/*
+ * Drop-in for torch_npu._npu_moe_token_unpermute_with_routing_map
+ * (npu_permute.py:23-30) and for upstream combine's unsort + K-way sum:
+ *   out[t] = sum_k w(t,k) * permuted[j(t,k)],  j(t,k) = position of flat
+ *   slot t*topk+k in sorted_indices, w = probs[t,k] (fp32, nullable -> 1).
+ * Accumulates in fp32, rounds to bf16 once.  permuted bf16 [T*topk, D],
+ * out bf16 [T, D].  Deterministic (fixed k order, no atomics).
+ */
+int ttamd_moe_token_unpermute(const void* permuted,
+                              const int32_t* sorted_indices,
+                              const float* probs, int64_t num_tokens,
+                              int64_t hidden, int topk, void* out,
+                              void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/*
+ * Same sum, given the inverse map (inverse[s] = position of flat slot s)
+ * that ttamd_moe_route returns; needs no workspace.
+ */
+int ttamd_moe_combine(const void* permuted, const int32_t* inverse,
+                      const float* probs, int64_t num_tokens, int64_t hidden,
+                      int topk, void* out, void* stream);
+
+/*
+ * Drop-in for torch_npu.npu_moe_token_unpermute_with_routing_map_grad
+ * (npu_permute.py:41-50):
+ *   grad_permuted[j] = w(s) * grad_out[s / topk],  s = sorted_indices[j],
+ *   w(s) = probs[s] (nullable -> 1), rounded to bf16 once.
+ * If grad_probs is non-null (and probs, permuted are given):
+ *   grad_probs[s] = <grad_out[s/topk], permuted[j]> accumulated in fp32.
+ */
+int ttamd_moe_token_unpermute_grad(const void* grad_out,
+                                   const int32_t* sorted_indices,
+                                   const float* probs, const void* permuted,
+                                   int64_t num_tokens, int64_t hidden,
+                                   int topk, void* grad_permuted,
+                                   float* grad_probs, void* stream);
+
+/*
+ * Row dot products: out[o(j)] = <a[j], b[b_index[j] / b_div]> in fp32,
+ * o(j) = out_by_index ? b_index[j] : j (b_index nullable -> j).
+ * Used for routing-score gradients.
+ */
+int ttamd_moe_rowdot(const void* a, const void* b, const int32_t* b_index,
+                     int b_div, int out_by_index, int64_t num_rows,
+                     int64_t num_b_rows, int64_t hidden, float* out,
+                     void* stream);
+
+/*
+ * Expert labels of rows laid out as num_groups consecutive groups
+ * (source rank r, local expert e), g = r * num_local_experts + e:
+ *   labels[j] = g(j) % num_local_experts, g(j) the group holding row j;
+ *   rows past sum(counts_group) get label num_local_experts.
+ * Replaces the label construction of NpuTokenDispatcher._permute
+ * (torchtitanturbo/models/common/npu_permute.py:68-72:
+ * arange(E_loc).repeat(ep).repeat_interleave(counts)), with no host sync.
+ * counts_group int32 [num_groups], num_groups <= 8192; labels int32 [rows].
+ */
+int ttamd_moe_group_labels(const int32_t* counts_group, int num_groups,
+                           int num_local_experts, int64_t num_rows,
+                           int32_t* labels, void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * Grouped GEMMs over ragged expert segments (bf16 in, fp32 accumulate).     *
+ * ------------------------------------------------------------------------ */
+
+/* Bytes of device workspace every ttamd_grouped_mm* call needs. */
+size_t ttamd_gemm_workspace_bytes(int64_t num_rows, int num_experts);
+
+/*
+ * out[m, n] = sum_k x[m, k] * w[e(m), n, k]  (bf16 out).
+ * Replaces torch._grouped_mm(x, w.transpose(-2,-1), offs)
+ * (torchtitanturbo/models/common/npu_gmm.py:17-18, :38).
+ * x [M, K], w [E, N, K], out [M, N]; N % 128 == 0, K % 64 == 0.
+ */
+int ttamd_grouped_mm(const void* x, const void* w, const int32_t* offs,
+                     int64_t num_rows, int num_experts, int64_t n, int64_t k,
+                     void* out, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/*
+ * Fused expert up-projection: h = x @ w13[e]^T (w13 [E, 2H, D], rows 0..H-1
+ * gate, H..2H-1 up), optional clamp (gate <= L, -L <= up <= L when
+ * swiglu_limit > 0), a = silu(gate) * up.
+ * Replaces npu_gmm.py:29-37 (cumsum, grouped_mm w13, clamp, npu_swiglu).
+ * x [M, D] -> a [M, H] bf16; h_out (nullable) receives the unclamped
+ * pre-activation bf16 [M, 2H] for the backward.  H % 64 == 0, D % 64 == 0.
+ * swiglu_limit: NaN = no clamp (the reference's swiglu_limit=None).
+ */
+int ttamd_grouped_mm_swiglu(const void* x, const void* w13,
+                            const int32_t* offs, int64_t num_rows,
+                            int num_experts, int64_t hidden, int64_t dim,
+                            float swiglu_limit, void* a_out, void* h_out,
+                            void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/*
+ * Fused expert down-projection + routing-weight scale + un-permute:
+ *   y[j] = a[j] @ w2[e(j)]^T  (w2 [E, D, H]),  fp32
+ *   v    = row_scale ? row_scale[j] * y[j] : y[j]
+ *   out[dest[j]] = bf16(v)   (dest nullable -> j)
+ * With dest = sorted_indices and topk = 1 this writes the combined layer
+ * output [T, D] directly; with topk > 1 it writes the flat-slot-ordered
+ * buffer that ttamd_moe_sum_topk reduces.  Replaces npu_gmm.py:38 plus the
+ * unsort/score multiply of upstream combine.  D % 128 == 0, H % 64 == 0.
+ */
+int ttamd_grouped_mm_unpermute(const void* a, const void* w2,
+                               const int32_t* offs, int64_t num_rows,
+                               int num_experts, int64_t dim, int64_t hidden,
+                               const float* row_scale, const int32_t* dest,
+                               int64_t num_dest_rows, void* out,
+                               void* workspace, size_t workspace_bytes,
+                               void* stream);
+
+/* out[t] = sum_{k<topk} in[t*topk + k] (fp32 accumulate, bf16 out). */
+int ttamd_moe_sum_topk(const void* in, int64_t num_tokens, int64_t hidden,
+                       int topk, void* out, void* stream);
+
+/*
+ * Grouped dgrad: dx[m, k] = sum_n dy[m, n] * w[e(m), n, k]  (bf16 out).
+ * Backward of ttamd_grouped_mm w.r.t. x; w [E, N, K] with K contiguous.
+ * N % 64 == 0, K % 128 == 0.
+ */
+int ttamd_grouped_mm_dgrad(const void* dy, const void* w, const int32_t* offs,
+                           int64_t num_rows, int num_experts, int64_t n,
+                           int64_t k, void* dx, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/*
+ * Grouped dgrad of the down projection fused with the SwiGLU backward:
+ *   g[m, p]  = sum_d dy[m, d] * w2[e(m), d, p]          (dA, fp32)
+ *   with h = [gate | up] from ttamd_grouped_mm_swiglu (h_out), L = limit:
+ *   gc = min(gate, L), uc = clamp(up, -L, L)   (identity when L <= 0)
+ *   dgate = g * uc * silu'(gc) * [gate <= L]
+ *   dup   = g * silu(gc)       * [-L <= up <= L]
+ *   dh[m] = [dgate | dup]  bf16 [M, 2H]
+ * a_out (nullable) receives silu(gc)*uc recomputed in bf16 [M, H].
+ * D % 64 == 0, H % 128 == 0; swiglu_limit NaN = no clamp.
+ */
+int ttamd_grouped_mm_dgrad_swiglu(const void* dy, const void* w2,
+                                  const void* h, const int32_t* offs,
+                                  int64_t num_rows, int num_experts,
+                                  int64_t dim, int64_t hidden,
+                                  float swiglu_limit, void* dh, void* a_out,
+                                  void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
+/*
+ * Grouped wgrad: dw[e, n, k] = sum_{m in group e} dy[m, n] * x[m, k].
+ * dy [M, N], x [M, K] bf16; dw [E, N, K] fp32 (dw_is_fp32=1) or bf16.
+ * Experts with no rows get zeros.  N % 128 == 0, K % 128 == 0.
+ * Deterministic (no atomics).
+ */
+int ttamd_grouped_mm_wgrad(const void* dy, const void* x, const int32_t* offs,
+                           int64_t num_rows, int num_experts, int64_t n,
+                           int64_t k, void* dw, int dw_is_fp32,
+                           void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TTAMD_MOE_H */

@@ -1,0 +1,347 @@
+"""CPU oracle of the MoE expert path -- TEST INFRASTRUCTURE ONLY.
+
+A numpy restatement of the reference path's algorithm, used as the checker
+by tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline leg.
+Nothing in the product (torchtitan-ascend_amd/) imports it; the product
+fails loudly without its HIP library instead of falling back to this code.
+
+Each function cites the reference (file:line under torchtitanturbo/) or the
+upstream TorchTitan behaviour it restates.  UPSTREAM marks TorchTitan code
+that the reference calls but does not vendor; it is restated from its
+public design.  How each function is pinned (the checks that do not merely
+retype it) is listed in PINNED below and exercised by tests/test_oracle_*.py.
+
+Numerics: inputs that are bf16 in the reference are converted exactly to
+fp32 (bf16 -> fp32 is exact); products are accumulated in fp32 (float64 for
+the reductions noted); values the reference materialises in bf16 (grouped
+GEMM outputs, SwiGLU output, dispatch rows with the score multiply) are
+rounded to bf16 at the same points, with round-to-nearest-even.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+# Function -> how it is pinned (see tests/test_oracle_*.py).
+PINNED = {
+    "stable_order": "brute-force Python loop; torch.argsort(stable=True) golden vectors; hypothesis invariants",
+    "histogram": "brute-force count; torch.bincount golden; sum == M",
+    "permute / unpermute": "round trip unpermute(permute(x)) == x; torch index_select/index_add golden",
+    "group_labels": "torch arange.repeat.repeat_interleave golden (npu_permute.py:68-72)",
+    "router_topk": "torch softmax/sigmoid + topk golden on tie-free inputs; explicit tie cases",
+    "experts_forward": "torch._grouped_mm golden; per-expert index_add loop and dense einsum forms",
+    "moe_forward": "per-token brute loop of model.py:703-735 form",
+    "moe_backward": "torch autograd of a torch fp32 restatement (golden); central finite differences",
+    "bf16_round": "torch .to(bfloat16) on random and special values",
+}
+
+
+# ---------------------------------------------------------------------------
+# bf16 helpers
+# ---------------------------------------------------------------------------
+def bf16_round(a: np.ndarray) -> np.ndarray:
+    """Round fp32 values to the nearest bf16 (ties to even); NaN stays NaN."""
+    a = np.asarray(a, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    lsb = (u >> 16) & 1
+    r = ((u + 0x7FFF + lsb) >> 16) << 16
+    out = r.astype(np.uint32).view(np.float32).copy()
+    nan = np.isnan(a)
+    out[nan] = np.nan
+    return out
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(a: np.ndarray) -> np.ndarray:
+    return (bf16_round(a).view(np.uint32) >> 16).astype(np.uint16)
+
+
+# ---------------------------------------------------------------------------
+# Routing (integer, bit-exact)
+# ---------------------------------------------------------------------------
+def histogram(labels: np.ndarray, num_experts: int) -> np.ndarray:
+    """counts[e] = #{s : labels[s] == e}.  UPSTREAM dispatch:
+    torch.histc(selected_experts_indices.view(-1), bins=E, min=0, max=E),
+    consumed at npu_gmm.py:29; labels outside [0, E) are not counted."""
+    lab = np.asarray(labels).reshape(-1).astype(np.int64)
+    valid = (lab >= 0) & (lab < num_experts)
+    return np.bincount(lab[valid], minlength=num_experts).astype(np.int32)
+
+
+def stable_order(labels: np.ndarray, num_experts: int) -> np.ndarray:
+    """Stable sort of the flat labels.  UPSTREAM dispatch:
+    torch.argsort(selected_experts_indices.view(-1), stable=True); also the
+    order torch_npu.npu_moe_token_permute produces (npu_permute.py:74-76).
+    Labels outside [0, E) are placed after every valid label, in input order."""
+    lab = np.asarray(labels).reshape(-1).astype(np.int64)
+    bucket = np.where((lab >= 0) & (lab < num_experts), lab, num_experts)
+    return np.argsort(bucket, kind="stable").astype(np.int32)
+
+
+def inverse_order(sorted_indices: np.ndarray) -> np.ndarray:
+    inv = np.empty_like(sorted_indices)
+    inv[sorted_indices] = np.arange(sorted_indices.size, dtype=sorted_indices.dtype)
+    return inv
+
+
+def offsets_from_counts(counts: np.ndarray) -> np.ndarray:
+    """Exclusive offsets [E+1]; offsets[1:] is the inclusive cumsum the
+    reference passes to grouped_mm (npu_gmm.py:29)."""
+    return np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+
+
+def permute(tokens: np.ndarray, labels: np.ndarray, top_k: int, num_experts: int):
+    """npu_moe_token_permute(tokens, indices) (npu_permute.py:74-76):
+    returns (permuted rows, sorted_indices) with permuted[j] = tokens[sorted[j] // K]."""
+    sidx = stable_order(labels, num_experts)
+    return np.asarray(tokens)[sidx // top_k], sidx
+
+
+def unpermute(permuted: np.ndarray, sorted_indices: np.ndarray, probs: np.ndarray | None, top_k: int):
+    """_npu_moe_token_unpermute_with_routing_map (npu_permute.py:23-30) and
+    UPSTREAM combine: out[t] = sum_k w(t,k) * permuted[pos(t,k)], fp32
+    accumulation in k order, bf16 result."""
+    p = np.asarray(permuted, dtype=np.float32)
+    M, D = p.shape
+    T = M // top_k
+    unsorted = np.empty_like(p)
+    unsorted[sorted_indices] = p
+    unsorted = unsorted.reshape(T, top_k, D)
+    w = np.ones((T, top_k), np.float32) if probs is None else np.asarray(probs, np.float32).reshape(T, top_k)
+    acc = np.zeros((T, D), np.float32)
+    for k in range(top_k):
+        acc += w[:, k, None] * unsorted[:, k]
+    return bf16_round(acc)
+
+
+def unpermute_grad(grad_out: np.ndarray, sorted_indices: np.ndarray, probs: np.ndarray | None, top_k: int,
+                   permuted: np.ndarray | None = None):
+    """npu_moe_token_unpermute_with_routing_map_grad (npu_permute.py:41-50):
+    grad_permuted[j] = w(s) * grad_out[s // K], s = sorted[j]; optional
+    grad_probs[s] = <grad_out[s // K], permuted[j]>."""
+    g = np.asarray(grad_out, np.float32)
+    s = np.asarray(sorted_indices)
+    w = np.ones(s.size, np.float32) if probs is None else np.asarray(probs, np.float32).reshape(-1)[s]
+    gp = bf16_round(g[s // top_k] * w[:, None])
+    gprobs = None
+    if permuted is not None:
+        gprobs = np.zeros(s.size, np.float32)
+        gprobs[s] = np.einsum("jd,jd->j", g[s // top_k].astype(np.float64),
+                              np.asarray(permuted, np.float64)).astype(np.float32)
+    return gp, gprobs
+
+
+def group_labels(counts_group: np.ndarray, num_local_experts: int, num_rows: int) -> np.ndarray:
+    """Labels of NpuTokenDispatcher._permute (npu_permute.py:68-72):
+    arange(E_loc).repeat(ep).repeat_interleave(counts_group); rows past the
+    total get label E_loc."""
+    cg = np.asarray(counts_group).reshape(-1)
+    ep = cg.size // num_local_experts
+    lab = np.repeat(np.tile(np.arange(num_local_experts), ep), cg)
+    out = np.full(num_rows, num_local_experts, dtype=np.int32)
+    n = min(num_rows, lab.size)
+    out[:n] = lab[:n]
+    return out
+
+
+def regroup_permute(routed_input: np.ndarray, counts_group: np.ndarray, ep_size: int, num_local_experts: int):
+    """NpuTokenDispatcher._permute (npu_permute.py:63-85): stable regroup of
+    rank-major rows into expert-major order.  Returns
+    (permuted, permuted_indices, num_tokens_per_expert)."""
+    labels = group_labels(counts_group, num_local_experts, routed_input.shape[0])
+    permuted, sidx = permute(routed_input, labels, 1, num_local_experts)
+    ntpe = np.asarray(counts_group).reshape(ep_size, -1).sum(0)
+    return permuted, sidx, ntpe
+
+
+# ---------------------------------------------------------------------------
+# Router top-k (UPSTREAM TokenChoiceTopKRouter; closed form in the reference
+# at models/qwen3_5/model.py:757-765)
+# ---------------------------------------------------------------------------
+def router_topk(logits: np.ndarray, top_k: int, score_func: str = "softmax", route_norm: bool = False,
+                route_scale: float = 1.0, expert_bias: np.ndarray | None = None, norm_eps: float = 1e-20):
+    """Scores in fp32 (softmax over experts or sigmoid); pick the top_k by
+    score (+ expert_bias for selection only), descending, ties to the lower
+    expert id; optional renormalisation by the sum of the picked scores
+    (model.py:762-764, UPSTREAM adds norm_eps); multiply by route_scale."""
+    z = np.asarray(logits, np.float32)
+    if score_func == "softmax":
+        m = z.max(axis=-1, keepdims=True)
+        e = np.exp((z - m).astype(np.float64))
+        s = (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+    elif score_func == "sigmoid":
+        s = (1.0 / (1.0 + np.exp(-z.astype(np.float64)))).astype(np.float32)
+    else:
+        raise ValueError(score_func)
+    sel = s if expert_bias is None else s + np.asarray(expert_bias, np.float32)
+    T, E = s.shape
+    # lexsort: primary key -sel (descending), secondary expert id (ascending)
+    order = np.lexsort((np.broadcast_to(np.arange(E), (T, E)), -sel), axis=-1)[:, :top_k]
+    top = np.take_along_axis(s, order, axis=-1).astype(np.float64)
+    if route_norm:
+        top = top / (top.sum(axis=-1, keepdims=True) + norm_eps)
+    top = top * route_scale
+    return top.astype(np.float32), order.astype(np.int64)
+
+
+# ---------------------------------------------------------------------------
+# Expert FFN (npu_gmm.py:21-40)
+# ---------------------------------------------------------------------------
+def silu(x: np.ndarray) -> np.ndarray:
+    x = np.asarray(x, np.float64)
+    return (x / (1.0 + np.exp(-x))).astype(np.float32)
+
+
+def grouped_mm(x: np.ndarray, w: np.ndarray, offs: np.ndarray) -> np.ndarray:
+    """torch._grouped_mm(x, w.transpose(-2, -1), offs) (npu_gmm.py:17-18):
+    out[m] = x[m] @ w[e(m)]^T for m in [offs[e-1], offs[e]), fp32 accumulate.
+    Rows past offs[-1] are left at zero."""
+    x = np.asarray(x, np.float32)
+    w = np.asarray(w, np.float32)
+    out = np.zeros((x.shape[0], w.shape[1]), np.float32)
+    start = 0
+    for e, end in enumerate(np.asarray(offs).tolist()):
+        if end > start:
+            out[start:end] = x[start:end] @ w[e].T
+        start = end
+    return out
+
+
+def swiglu(h: np.ndarray, swiglu_limit: float | None = None) -> np.ndarray:
+    """Clamp (npu_gmm.py:32-36) then npu_swiglu (npu_gmm.py:37):
+    gate = first half, up = second half; silu(gate) * up."""
+    H = h.shape[-1] // 2
+    gate, up = h[..., :H], h[..., H:]
+    if swiglu_limit is not None:
+        up = np.clip(up, -swiglu_limit, swiglu_limit)
+        gate = np.minimum(gate, swiglu_limit)
+    return (silu(gate) * up).astype(np.float32)
+
+
+def experts_forward(x: np.ndarray, w13: np.ndarray, w2: np.ndarray, counts: np.ndarray,
+                    swiglu_limit: float | None = None, round_intermediates: bool = True):
+    """_run_experts_grouped_mm (npu_gmm.py:21-40) on routed rows x [M, D].
+    Returns (y [M, D], h [M, 2H], a [M, H]); with round_intermediates the
+    grouped GEMM outputs and the SwiGLU output are rounded to bf16 where the
+    reference materialises them in bf16."""
+    offs = np.cumsum(counts).astype(np.int64)
+    h = grouped_mm(x, w13, offs)
+    if round_intermediates:
+        h = bf16_round(h)
+    a = swiglu(h, swiglu_limit)
+    if round_intermediates:
+        a = bf16_round(a)
+    y = grouped_mm(a, w2, offs)
+    if round_intermediates:
+        y = bf16_round(y)
+    return y, h, a
+
+
+def moe_forward(x: np.ndarray, top_scores: np.ndarray, idx: np.ndarray, w13: np.ndarray, w2: np.ndarray,
+                num_experts: int, score_before_experts: bool, swiglu_limit: float | None = None,
+                round_intermediates: bool = True) -> np.ndarray:
+    """NpuGroupedExperts.forward (npu_gmm.py:100-110): UPSTREAM dispatch
+    (gather in stable expert order, fp32 score multiply before the experts
+    if score_before_experts), experts, UPSTREAM combine (score multiply after
+    the experts otherwise, K-way sum).  x [T, D] -> [T, D]."""
+    T, D = x.shape
+    K = top_scores.shape[-1]
+    flat_scores = np.asarray(top_scores, np.float32).reshape(-1)
+    sidx = stable_order(idx, num_experts)
+    counts = histogram(idx, num_experts)
+    routed = np.asarray(x, np.float32)[sidx // K]
+    if score_before_experts:
+        routed = routed * flat_scores[sidx][:, None]
+        if round_intermediates:
+            routed = bf16_round(routed)
+    y, _, _ = experts_forward(routed, w13, w2, counts, swiglu_limit, round_intermediates)
+    probs = None if score_before_experts else flat_scores
+    return unpermute(y, sidx, probs, K) if round_intermediates else _unpermute_f32(y, sidx, probs, K)
+
+
+def _unpermute_f32(y, sidx, probs, K):
+    M, D = y.shape
+    un = np.empty_like(y)
+    un[sidx] = y
+    un = un.reshape(M // K, K, D)
+    w = np.ones((M // K, K), np.float32) if probs is None else probs.reshape(M // K, K)
+    return (un * w[..., None]).sum(1).astype(np.float32)
+
+
+def moe_backward(x, top_scores, idx, w13, w2, num_experts, score_before_experts, dout,
+                 swiglu_limit: float | None = None):
+    """Gradients of moe_forward (fp32 throughout, no intermediate rounding):
+    returns dict(dx [T,D], dscores [T,K], dw13 [E,2H,D], dw2 [E,D,H]).
+    The chain is the autograd of npu_gmm.py:21-40 plus the UPSTREAM
+    dispatch/combine score multiplies."""
+    x = np.asarray(x, np.float32)
+    T, D = x.shape
+    K = top_scores.shape[-1]
+    E = num_experts
+    H = w2.shape[-1]
+    s_flat = np.asarray(top_scores, np.float32).reshape(-1)
+    sidx = stable_order(idx, E)
+    counts = histogram(idx, E)
+    offs = np.cumsum(counts)
+    tok = sidx // K
+    xr = x[tok]
+    routed = xr * s_flat[sidx][:, None] if score_before_experts else xr
+    h = grouped_mm(routed, w13, offs)
+    a = swiglu(h, swiglu_limit)
+    y = grouped_mm(a, w2, offs)
+    dout = np.asarray(dout, np.float32)
+    g_tok = dout[tok]  # dOut gathered per routed row
+    dscores = np.zeros(T * K, np.float32)
+    if score_before_experts:
+        dy = g_tok
+    else:
+        dy = g_tok * s_flat[sidx][:, None]
+        dscores[sidx] = np.einsum("jd,jd->j", g_tok.astype(np.float64), y.astype(np.float64))
+    dw2 = np.zeros_like(np.asarray(w2, np.float32))
+    dw13 = np.zeros_like(np.asarray(w13, np.float32))
+    da = np.zeros_like(a)
+    start = 0
+    for e, end in enumerate(offs.tolist()):
+        if end > start:
+            dw2[e] = dy[start:end].T @ a[start:end]
+            da[start:end] = dy[start:end] @ np.asarray(w2[e], np.float32)
+        start = end
+    gate, up = h[:, :H], h[:, H:]
+    gc, uc = gate, up
+    mg = np.ones_like(gate)
+    mu = np.ones_like(up)
+    if swiglu_limit is not None:
+        mg = (gate <= swiglu_limit).astype(np.float32)
+        mu = ((up >= -swiglu_limit) & (up <= swiglu_limit)).astype(np.float32)
+        gc = np.minimum(gate, swiglu_limit)
+        uc = np.clip(up, -swiglu_limit, swiglu_limit)
+    sig = (1.0 / (1.0 + np.exp(-gc.astype(np.float64)))).astype(np.float32)
+    dsilu = sig * (1.0 + gc * (1.0 - sig))
+    dh = np.concatenate([da * uc * dsilu * mg, da * gc * sig * mu], axis=1).astype(np.float32)
+    d_routed = np.zeros_like(routed)
+    start = 0
+    for e, end in enumerate(offs.tolist()):
+        if end > start:
+            dw13[e] = dh[start:end].T @ routed[start:end]
+            d_routed[start:end] = dh[start:end] @ np.asarray(w13[e], np.float32)
+        start = end
+    dx = np.zeros_like(x)
+    if score_before_experts:
+        dscores[sidx] = np.einsum("jd,jd->j", d_routed.astype(np.float64), xr.astype(np.float64))
+        np.add.at(dx, tok, d_routed * s_flat[sidx][:, None])
+    else:
+        np.add.at(dx, tok, d_routed)
+    return {"dx": dx, "dscores": dscores.reshape(T, K), "dw13": dw13, "dw2": dw2}
+
+
+def max_rel_err(got: np.ndarray, ref: np.ndarray) -> float:
+    """max |got - ref| / max |ref| (the norm-wise relative error the
+    tolerances 2e-2 / 5e-2 are stated in)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    denom = np.abs(ref).max()
+    if denom == 0:
+        return float(np.abs(got).max())
+    return float(np.abs(got - ref).max() / denom)

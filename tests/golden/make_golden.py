@@ -1,0 +1,213 @@
+"""Write the golden fixtures under tests/golden/ from torch's own CPU routines.
+
+The fixtures pin the CPU oracle (oracle/moe_oracle.py) against computations
+that do not share its code: torch.argsort(stable=True), torch.bincount,
+torch.topk, torch._grouped_mm (the op the reference calls,
+torchtitanturbo/models/common/npu_gmm.py:17-18) and torch autograd.
+The reference itself cannot run here (it imports torch_npu and torchtitan,
+neither installed), so no fixture comes from it.
+
+Run:  python tests/golden/make_golden.py      (writes *.npz, no pickles)
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+OUT = Path(__file__).resolve().parent
+
+
+def _save(name: str, **arrays):
+    np.savez_compressed(OUT / f"{name}.npz", **{k: np.asarray(v) for k, v in arrays.items()})
+
+
+def _bf16(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.bfloat16)
+
+
+def routing_cases():
+    cases = {}
+    g = torch.Generator().manual_seed(0)
+    specs = [
+        ("uniform", 64, 4, 8),
+        ("skewed", 96, 2, 16),
+        ("single_expert", 40, 1, 8),
+        ("empty_experts", 50, 2, 32),
+        ("top8_e128", 32, 8, 128),
+        ("one_token", 1, 4, 8),
+    ]
+    for name, T, K, E in specs:
+        if name == "skewed":
+            p = torch.tensor([0.5 ** i for i in range(E)])
+            lab = torch.multinomial(p / p.sum(), T * K, replacement=True, generator=g).view(T, K)
+        elif name == "single_expert":
+            lab = torch.full((T, K), 3, dtype=torch.int64)
+        elif name == "empty_experts":
+            lab = torch.randint(0, 4, (T, K), generator=g) * 5  # only experts 0,5,10,15
+        else:
+            lab = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+        flat = lab.reshape(-1)
+        cases[name] = dict(
+            labels=lab.numpy().astype(np.int64),
+            num_experts=np.int64(E),
+            sorted_indices=torch.argsort(flat, stable=True).numpy().astype(np.int32),
+            counts=torch.bincount(flat, minlength=E).numpy().astype(np.int32),
+        )
+    # labels outside [0, E): this build sorts them after every valid label
+    lab = torch.tensor([[2, -1], [7, 0], [2, 9], [1, 2]], dtype=torch.int64)
+    E = 8
+    flat = lab.reshape(-1)
+    bucket = torch.where((flat >= 0) & (flat < E), flat, torch.full_like(flat, E))
+    cases["invalid_labels_sort_last"] = dict(
+        labels=lab.numpy(), num_experts=np.int64(E),
+        sorted_indices=torch.argsort(bucket, stable=True).numpy().astype(np.int32),
+        counts=torch.bincount(flat[(flat >= 0) & (flat < E)], minlength=E).numpy().astype(np.int32),
+    )
+    for name, arr in cases.items():
+        _save(f"routing_{name}", **arr)
+
+
+def permute_cases():
+    g = torch.Generator().manual_seed(1)
+    T, K, E, D = 24, 2, 6, 16
+    tokens = _bf16(torch.randn(T, D, generator=g))
+    lab = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    probs = torch.rand(T, K, generator=g)
+    flat = lab.reshape(-1)
+    sidx = torch.argsort(flat, stable=True)
+    permuted = tokens.index_select(0, sidx // K)
+    # unpermute: index_copy back to slot order, weight, sum over K (fp32)
+    un = torch.zeros(T * K, D)
+    un.index_copy_(0, sidx, permuted.float())
+    out = (un.view(T, K, D) * probs.unsqueeze(-1)).sum(1)
+    out_noprob = un.view(T, K, D).sum(1)
+    _save(
+        "permute_basic", tokens=tokens.float().numpy(), labels=lab.numpy(), probs=probs.numpy(),
+        num_experts=np.int64(E), top_k=np.int64(K), permuted=permuted.float().numpy(),
+        sorted_indices=sidx.numpy().astype(np.int32), unpermuted=_bf16(out).float().numpy(),
+        unpermuted_noprob=_bf16(out_noprob).float().numpy(),
+    )
+    # regroup labels of NpuTokenDispatcher._permute (npu_permute.py:68-72)
+    ep, E_loc = 3, 4
+    counts_group = torch.randint(0, 5, (ep * E_loc,), generator=g)
+    counts_group[5] = 0
+    labels = torch.arange(E_loc).repeat(ep).repeat_interleave(counts_group)
+    _save("regroup_labels", counts_group=counts_group.numpy(), ep=np.int64(ep), num_local_experts=np.int64(E_loc),
+          labels=labels.numpy().astype(np.int32))
+
+
+def router_cases():
+    g = torch.Generator().manual_seed(2)
+    T, E = 64, 16
+    # tie-free logits: distinct values with gaps well above fp32 rounding
+    logits = torch.stack([torch.randperm(E, generator=g).float() * 0.37 - 3.0 for _ in range(T)])
+    logits = logits + 0.01 * torch.randn(T, E, generator=g)
+    bias = torch.randn(E, generator=g) * 0.05
+    for func in ("softmax", "sigmoid"):
+        s = torch.softmax(logits, dim=-1) if func == "softmax" else torch.sigmoid(logits)
+        for K, norm in ((1, False), (4, True), (4, False)):
+            v, i = torch.topk(s, K, dim=-1)
+            if norm:
+                v = v / (v.sum(-1, keepdim=True) + 1e-20)
+            _, ib = torch.topk(s + bias, K, dim=-1)
+            vb = s.gather(1, ib)
+            _save(f"router_{func}_k{K}_{'norm' if norm else 'raw'}", logits=logits.numpy(), top_k=np.int64(K),
+                  scores=v.numpy(), indices=i.numpy(), bias=bias.numpy(), scores_bias=vb.numpy(),
+                  indices_bias=ib.numpy())
+
+
+def experts_cases():
+    """The reference's op sequence (npu_gmm.py:29-38) on CPU torch, bf16."""
+    g = torch.Generator().manual_seed(3)
+    E, D, H = 4, 64, 32
+    counts = torch.tensor([5, 0, 11, 3], dtype=torch.int64)
+    M = int(counts.sum())
+    x = _bf16(torch.randn(M, D, generator=g))
+    w13 = _bf16(torch.randn(E, 2 * H, D, generator=g) * 0.1)
+    w2 = _bf16(torch.randn(E, D, H, generator=g) * 0.1)
+    offs = torch.cumsum(counts, 0, dtype=torch.int32)
+    for limit in (None, 0.5):
+        h = torch._grouped_mm(x, w13.transpose(-2, -1), offs)
+        if limit is not None:
+            gate, up = h.chunk(2, -1)
+            up = torch.clamp(up, min=-limit, max=limit)
+            gate = torch.clamp(gate, max=limit)
+            h = torch.cat([gate, up], dim=-1)
+        gate, up = h.chunk(2, -1)
+        a = (F.silu(gate.float()) * up.float()).to(torch.bfloat16)
+        y = torch._grouped_mm(a, w2.transpose(-2, -1), offs)
+        # fp32 version of the same chain
+        h32 = torch.cat([x[s:e].float() @ w13[i].float().T for i, (s, e) in enumerate(zip([0, *offs[:-1].tolist()], offs.tolist()))])
+        _save(
+            f"experts_{'limit' if limit is not None else 'nolimit'}", x=x.float().numpy(), w13=w13.float().numpy(),
+            w2=w2.float().numpy(), counts=counts.numpy(), limit=np.float64(np.nan if limit is None else limit),
+            h_bf16=h.float().numpy(), a_bf16=a.float().numpy(), y_bf16=y.float().numpy(), h_f32=h32.numpy(),
+        )
+
+
+def layer_cases():
+    """Whole layer fwd + bwd through torch autograd on an fp32 restatement
+    (dispatch gather, per-expert F.linear, combine with index_add_ in the
+    form of torchtitanturbo/models/qwen3_5/model.py:703-735)."""
+    g = torch.Generator().manual_seed(4)
+    for name, (T, K, E, D, H, score_before, limit) in {
+        "k2_after": (16, 2, 4, 32, 16, False, None),
+        "k1_before": (20, 1, 4, 32, 16, True, None),
+        "k2_after_limit": (16, 2, 4, 32, 16, False, 0.3),
+    }.items():
+        x = torch.randn(T, D, generator=g)
+        w13 = torch.randn(E, 2 * H, D, generator=g) * 0.2
+        w2 = torch.randn(E, D, H, generator=g) * 0.2
+        idx = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+        scores = torch.rand(T, K, generator=g) + 0.1
+        dout = torch.randn(T, D, generator=g)
+        xs, w13s, w2s, ss = (t.clone().requires_grad_(True) for t in (x, w13, w2, scores))
+        out = torch.zeros(T, D)
+        for e in range(E):
+            tk, kk = torch.where(idx == e)
+            if tk.numel() == 0:
+                continue
+            xi = xs[tk]
+            if score_before:
+                xi = xi * ss[tk, kk, None]
+            h = F.linear(xi, w13s[e])
+            gate, up = h.chunk(2, -1)
+            if limit is not None:
+                up = torch.clamp(up, min=-limit, max=limit)
+                gate = torch.clamp(gate, max=limit)
+            yi = F.linear(F.silu(gate) * up, w2s[e])
+            if not score_before:
+                yi = yi * ss[tk, kk, None]
+            out = out.index_add(0, tk, yi)
+        out.backward(dout)
+        _save(
+            f"layer_{name}", x=x.numpy(), w13=w13.numpy(), w2=w2.numpy(), idx=idx.numpy(), scores=scores.numpy(),
+            dout=dout.numpy(), num_experts=np.int64(E), score_before=np.int64(score_before),
+            limit=np.float64(np.nan if limit is None else limit), out=out.detach().numpy(),
+            dx=xs.grad.numpy(), dw13=w13s.grad.numpy(), dw2=w2s.grad.numpy(), dscores=ss.grad.numpy(),
+        )
+
+
+def bf16_cases():
+    g = torch.Generator().manual_seed(5)
+    v = torch.cat([
+        torch.randn(4096, generator=g) * 10.0 ** torch.randint(-6, 6, (4096,), generator=g).float(),
+        torch.tensor([0.0, -0.0, 1.0, -1.0, 65504.0, 3.4e38, 1e-40, float("inf"), float("-inf")]),
+        # exact ties between two bf16 neighbours
+        torch.tensor([1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, -(1.0 + 2.0 ** -8)]),
+    ])
+    _save("bf16_round", values=v.numpy(), rounded=v.to(torch.bfloat16).float().numpy())
+
+
+if __name__ == "__main__":
+    torch.manual_seed(0)
+    routing_cases()
+    permute_cases()
+    router_cases()
+    experts_cases()
+    layer_cases()
+    bf16_cases()
+    print("torch", torch.__version__, "->", sorted(p.name for p in OUT.glob("*.npz")))

@@ -1,0 +1,107 @@
+"""The C-ABI library loads and exports what include/ttamd_moe.h declares (CPU).
+
+Only calls that the host-side validation rejects are made here: they return
+TTAMD_EINVAL before anything touches a GPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import importlib
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "ttamd_moe.h"
+_lib = importlib.import_module("torchtitan-ascend_amd._lib")
+
+
+def header_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ttamd_\w+)\s*\(", text)))
+
+
+def test_header_declares_functions():
+    names = header_functions()
+    assert "ttamd_moe_route" in names and "ttamd_grouped_mm_swiglu" in names
+    assert len(names) >= 20
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    for name in header_functions():
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+
+
+def test_binding_covers_header():
+    assert sorted(_lib.SIGNATURES) == header_functions()
+
+
+def test_abi_version():
+    assert _lib.load().ttamd_abi_version() == _lib.ABI_VERSION
+
+
+def _err(rc):
+    assert rc == 1, rc
+    return _lib.load().ttamd_last_error().decode()
+
+
+def test_route_rejects_bad_arguments():
+    lib = _lib.load()
+    ws = ctypes.c_void_p(16)
+    # too many experts
+    msg = _err(lib.ttamd_moe_route(ctypes.c_void_p(16), 1, 8, 5000, None, None, None, ctypes.c_void_p(16), None,
+                                   None, ws, 1 << 20, None))
+    assert "num_experts" in msg
+    # missing workspace
+    msg = _err(lib.ttamd_moe_route(ctypes.c_void_p(16), 1, 8, 4, None, None, None, ctypes.c_void_p(16), None,
+                                   None, None, 0, None))
+    assert "workspace" in msg
+    # scores without sorted_scores
+    msg = _err(lib.ttamd_moe_route(ctypes.c_void_p(16), 1, 8, 4, ctypes.c_void_p(16), None, None,
+                                   ctypes.c_void_p(16), None, None, ws, 1 << 20, None))
+    assert "sorted_scores" in msg
+
+
+def test_gemm_rejects_bad_shapes():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    ws = lib.ttamd_gemm_workspace_bytes(1024, 8)
+    assert ws >= 16 * (1024 // 128 + 8)
+    msg = _err(lib.ttamd_grouped_mm(p, p, p, 1024, 8, 100, 64, p, p, ws, None))
+    assert "multiple of 128" in msg
+    msg = _err(lib.ttamd_grouped_mm_swiglu(p, p, p, 1024, 8, 96, 256, float("nan"), p, None, p, ws, None))
+    assert "hidden" in msg
+    msg = _err(lib.ttamd_grouped_mm_swiglu(p, p, p, 1024, 8, 128, 256, -1.0, p, None, p, ws, None))
+    assert "swiglu_limit" in msg
+    msg = _err(lib.ttamd_grouped_mm(ctypes.c_void_p(258), p, p, 1024, 8, 128, 64, p, p, ws, None))
+    assert "aligned" in msg
+    msg = _err(lib.ttamd_grouped_mm(p, p, None, 1024, 8, 128, 64, p, p, ws, None))
+    assert "offs" in msg
+    msg = _err(lib.ttamd_grouped_mm(p, p, p, 1024, 8, 128, 64, p, p, 8, None))
+    assert "workspace" in msg
+
+
+def test_rows_reject_bad_hidden():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    msg = _err(lib.ttamd_moe_gather_rows(p, p, None, 10, 10, 12, 1, p, None))
+    assert "hidden" in msg
+    msg = _err(lib.ttamd_moe_combine(p, p, None, 10, 64, 0, p, None))
+    assert "topk" in msg
+    msg = _err(lib.ttamd_moe_group_labels(p, 6, 4, 10, p, None))
+    assert "multiple" in msg
+
+
+def test_router_topk_rejects_bad_k():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    msg = _err(lib.ttamd_router_topk(p, None, 4, 8, 9, 0, 0, 0.0, 1.0, p, p, None))
+    assert "topk" in msg
+
+
+@pytest.mark.parametrize("fn", ["ttamd_route_workspace_bytes", "ttamd_gemm_workspace_bytes"])
+def test_workspace_queries_reject_negative(fn):
+    assert getattr(_lib.load(), fn)(-1, 4) == 0

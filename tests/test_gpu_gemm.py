@@ -1,0 +1,207 @@
+"""GPU parity of the grouped GEMM kernels against the CPU oracle (fp32
+accumulation).  Tolerance: max relative error (max|got-ref| / max|ref|)
+<= 2e-2 for bf16, the bound the path is specified to."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import DEV, announce, bf16_dev, f32_dev, rand_bf16, to_np, zipf_counts
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _counts(kind, M, E, rng):
+    if kind == "uniform":
+        c = np.full(E, M // E)
+        c[: M - c.sum()] += 1
+        return c
+    if kind == "random":
+        cut = np.sort(rng.integers(0, M + 1, E - 1))
+        return np.diff(np.concatenate([[0], cut, [M]]))
+    if kind == "zipf":
+        return zipf_counts(M, E, 1.2, max(1, E - E // 8), rng)
+    if kind == "one":
+        c = np.zeros(E, np.int64)
+        c[E // 2] = M
+        return c
+    raise ValueError(kind)
+
+
+def _offs(counts):
+    return torch.from_numpy(np.cumsum(counts).astype(np.int32)).to(DEV)
+
+
+def _gmm_ref(x, w, counts):
+    return O.grouped_mm(x, w, np.cumsum(counts))
+
+
+CASES = [
+    # M, E, N, K, kind
+    (1000, 8, 256, 256, "random"),
+    (700, 4, 512, 2048, "zipf"),
+    (129, 3, 128, 64, "random"),
+    (4096, 16, 384, 512, "one"),
+    (333, 32, 128, 128, "zipf"),
+]
+
+
+@pytest.mark.parametrize("M,E,N,K,kind", CASES)
+def test_grouped_mm(ops, M, E, N, K, kind):
+    rng = np.random.default_rng(M + E + N + K)
+    counts = _counts(kind, M, E, rng)
+    x = rand_bf16(rng, (M, K))
+    w = rand_bf16(rng, (E, N, K), 0.05)
+    announce(f"grouped_mm M={M} E={E} N={N} K={K} {kind}")
+    out = ops.grouped_mm(bf16_dev(x), bf16_dev(w), _offs(counts))
+    ref = _gmm_ref(x, w, counts)
+    assert O.max_rel_err(to_np(out), ref) < TOL
+
+
+def test_grouped_mm_ignores_rows_past_last_offset(ops):
+    rng = np.random.default_rng(1)
+    M, E, N, K = 512, 4, 128, 128
+    counts = np.array([100, 0, 200, 50])  # 350 of 512 rows grouped
+    x = rand_bf16(rng, (M, K))
+    w = rand_bf16(rng, (E, N, K), 0.05)
+    announce("grouped_mm tail rows")
+    out = torch.full((M, N), 7.0, dtype=torch.bfloat16, device=DEV)
+    res = ops.grouped_mm(bf16_dev(x), bf16_dev(w), _offs(counts))
+    out[:350] = res[:350]
+    assert O.max_rel_err(to_np(res)[:350], _gmm_ref(x, w, counts)[:350]) < TOL
+
+
+@pytest.mark.parametrize("limit", [None, 0.75])
+@pytest.mark.parametrize("M,E,D,H,kind", [(1000, 8, 256, 128, "random"), (2048, 16, 512, 192, "zipf"),
+                                          (96, 2, 128, 64, "one")])
+def test_grouped_mm_swiglu(ops, M, E, D, H, kind, limit):
+    rng = np.random.default_rng(M + D + H)
+    counts = _counts(kind, M, E, rng)
+    x = rand_bf16(rng, (M, D))
+    w13 = rand_bf16(rng, (E, 2 * H, D), 0.08)
+    announce(f"swiglu M={M} E={E} D={D} H={H} {kind} limit={limit}")
+    a, h = ops.grouped_mm_swiglu(bf16_dev(x), bf16_dev(w13), _offs(counts), limit, save_h=True)
+    h_ref = O.bf16_round(_gmm_ref(x, w13, counts))
+    a_ref = O.swiglu(h_ref, limit)
+    assert O.max_rel_err(to_np(h), h_ref) < TOL
+    assert O.max_rel_err(to_np(a), a_ref) < TOL
+    # the activation is computed from the bf16 pre-activation the kernel stored
+    assert O.max_rel_err(to_np(a), O.swiglu(to_np(h), limit)) < 1e-2
+
+
+@pytest.mark.parametrize("topk", [1, 4])
+def test_grouped_mm_unpermute_scatter_scale(ops, topk):
+    rng = np.random.default_rng(topk)
+    T, E, D, H = 300, 8, 256, 128
+    M = T * topk
+    counts = _counts("random", M, E, rng)
+    a = rand_bf16(rng, (M, H))
+    w2 = rand_bf16(rng, (E, D, H), 0.08)
+    dest = rng.permutation(M).astype(np.int32)
+    scale = rng.random(M).astype(np.float32)
+    announce(f"unpermute scatter topk={topk}")
+    out = ops.grouped_mm_unpermute(bf16_dev(a), bf16_dev(w2), _offs(counts), f32_dev(scale),
+                                   torch.from_numpy(dest).to(DEV), M)
+    y = _gmm_ref(a, w2, counts) * scale[:, None]
+    ref = np.zeros_like(y)
+    ref[dest] = y
+    assert O.max_rel_err(to_np(out), ref) < TOL
+    if topk > 1:
+        summed = ops.sum_topk(out, topk)
+        assert O.max_rel_err(to_np(summed), ref.reshape(T, topk, D).sum(1)) < TOL
+
+
+@pytest.mark.parametrize("M,E,N,K,kind", [(1000, 8, 256, 256, "random"), (700, 4, 1536, 2048, "zipf"),
+                                          (200, 5, 64, 384, "random")])
+def test_grouped_mm_dgrad(ops, M, E, N, K, kind):
+    rng = np.random.default_rng(M * 3 + N)
+    counts = _counts(kind, M, E, rng)
+    dy = rand_bf16(rng, (M, N))
+    w = rand_bf16(rng, (E, N, K), 0.05)
+    announce(f"dgrad M={M} E={E} N={N} K={K}")
+    dx = ops.grouped_mm_dgrad(bf16_dev(dy), bf16_dev(w), _offs(counts))
+    offs = np.cumsum(counts)
+    ref = np.zeros((M, K), np.float32)
+    s = 0
+    for e, t in enumerate(offs):
+        ref[s:t] = dy[s:t] @ w[e]
+        s = t
+    assert O.max_rel_err(to_np(dx), ref) < TOL
+
+
+@pytest.mark.parametrize("limit", [None, 0.5])
+def test_grouped_mm_dgrad_swiglu(ops, limit):
+    rng = np.random.default_rng(77)
+    M, E, D, H = 900, 6, 256, 256
+    counts = _counts("random", M, E, rng)
+    dy = rand_bf16(rng, (M, D))
+    w2 = rand_bf16(rng, (E, D, H), 0.08)
+    h = rand_bf16(rng, (M, 2 * H))
+    announce(f"dgrad_swiglu limit={limit}")
+    dh, a = ops.grouped_mm_dgrad_swiglu(bf16_dev(dy), bf16_dev(w2), bf16_dev(h), _offs(counts), limit, want_a=True)
+    offs = np.cumsum(counts)
+    g = np.zeros((M, H), np.float32)
+    s = 0
+    for e, t in enumerate(offs):
+        g[s:t] = dy[s:t] @ w2[e]
+        s = t
+    gate, up = h[:, :H], h[:, H:]
+    mg = np.ones_like(gate)
+    mu = np.ones_like(up)
+    gc, uc = gate, up
+    if limit is not None:
+        mg = (gate <= limit).astype(np.float32)
+        mu = ((up >= -limit) & (up <= limit)).astype(np.float32)
+        gc, uc = np.minimum(gate, limit), np.clip(up, -limit, limit)
+    sig = 1 / (1 + np.exp(-gc.astype(np.float64)))
+    ref = np.concatenate([g * uc * sig * (1 + gc * (1 - sig)) * mg, g * gc * sig * mu], axis=1)
+    got = to_np(dh)
+    n = int(offs[-1])
+    assert O.max_rel_err(got[:n, :H], ref[:n, :H]) < TOL
+    assert O.max_rel_err(got[:n, H:], ref[:n, H:]) < TOL
+    assert O.max_rel_err(to_np(a)[:n], O.swiglu(h, limit)[:n]) < 1e-2
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,E,N,K,kind", [(1000, 8, 256, 128, "random"), (3000, 32, 128, 256, "zipf"),
+                                          (64, 4, 128, 128, "one")])
+def test_grouped_mm_wgrad(ops, M, E, N, K, kind, out_dtype):
+    rng = np.random.default_rng(M + E * 5)
+    counts = _counts(kind, M, E, rng)
+    dy = rand_bf16(rng, (M, N))
+    x = rand_bf16(rng, (M, K))
+    announce(f"wgrad M={M} E={E} N={N} K={K} {kind} {out_dtype}")
+    dw = ops.grouped_mm_wgrad(bf16_dev(dy), bf16_dev(x), _offs(counts), E, out_dtype)
+    offs = np.cumsum(counts)
+    ref = np.zeros((E, N, K), np.float32)
+    s = 0
+    for e, t in enumerate(offs):
+        ref[e] = dy[s:t].T @ x[s:t]
+        s = t
+    got = to_np(dw)
+    assert O.max_rel_err(got, ref) < (1e-5 if out_dtype == torch.float32 and M < 128 else TOL)
+    for e in np.where(counts == 0)[0]:  # empty experts get exact zeros
+        assert not np.any(got[e])
+
+
+def test_grouped_mm_full_size_linearity_and_samples(ops):
+    """Qwen3-30B-A3B w13 at full size (M=65536, E=128, N=1536, K=2048):
+    scaling x by 2 scales the output exactly, and sampled rows match the oracle."""
+    rng = np.random.default_rng(2)
+    M, E, N, K = 65536, 128, 1536, 2048
+    counts = _counts("uniform", M, E, rng)
+    x = torch.randn(M, K, device=DEV).to(torch.bfloat16)
+    w = (torch.randn(E, N, K, device=DEV) * 0.02).to(torch.bfloat16)
+    offs = _offs(counts)
+    announce("grouped_mm full size")
+    out = ops.grouped_mm(x, w, offs)
+    out2 = ops.grouped_mm(x * 2, w, offs)
+    assert torch.equal(out2, out * 2)
+    rows = np.sort(rng.choice(M, 64, replace=False))
+    e_of = np.searchsorted(np.cumsum(counts), rows, side="right")
+    xs = to_np(x[torch.from_numpy(rows).to(DEV)])
+    ref = np.stack([xs[i] @ to_np(w[int(e)]).T for i, e in enumerate(e_of)])
+    assert O.max_rel_err(to_np(out[torch.from_numpy(rows).to(DEV)]), ref) < TOL

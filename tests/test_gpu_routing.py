@@ -1,0 +1,206 @@
+"""GPU parity of the routing kernels (router top-k, histogram, stable sort,
+permute / unpermute / regroup) against the CPU oracle.  Index outputs are
+compared bit-exactly; row moves without arithmetic are bit-exact too."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden_names, load_golden
+from gpu_util import DEV, announce, bf16_dev, f32_dev, rand_bf16, to_np, topk_labels, zipf_counts, labels_from_counts
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_route(ops, labels_np, E, dtype=torch.int64, scores=None):
+    lab = torch.from_numpy(np.ascontiguousarray(labels_np)).to(dtype).to(DEV)
+    r = ops.route(lab, E, None if scores is None else f32_dev(scores))
+    sidx = O.stable_order(labels_np, E)
+    counts = O.histogram(labels_np, E)
+    np.testing.assert_array_equal(r.sorted_indices.cpu().numpy(), sidx)
+    np.testing.assert_array_equal(r.counts.cpu().numpy(), counts)
+    off = O.offsets_from_counts(counts)
+    np.testing.assert_array_equal(r.offsets.cpu().numpy()[:E], off[:E])
+    np.testing.assert_array_equal(r.inverse.cpu().numpy(), O.inverse_order(sidx))
+    if scores is not None:
+        np.testing.assert_array_equal(r.sorted_scores.cpu().numpy(), np.asarray(scores, np.float32).reshape(-1)[sidx])
+    return r
+
+
+@pytest.mark.parametrize("name", golden_names("routing_"))
+def test_route_golden(ops, name):
+    g = load_golden(name)
+    announce(f"route golden {name}")
+    E = int(g["num_experts"])
+    r = _check_route(ops, g["labels"], E)
+    np.testing.assert_array_equal(r.sorted_indices.cpu().numpy(), g["sorted_indices"])
+
+
+@pytest.mark.parametrize(
+    "T,K,E,dtype",
+    [
+        (8192, 8, 128, torch.int64),  # Qwen3-30B-A3B shape
+        (8192, 8, 128, torch.int32),
+        (2048, 1, 8, torch.int64),  # Llama4 debug (config 1)
+        (8192, 1, 16, torch.int64),  # Llama4 Scout (config 3)
+        (3, 2, 1024, torch.int64),
+        (1000, 6, 64, torch.int32),
+    ],
+)
+def test_route_uniform_bit_exact(ops, T, K, E, dtype):
+    rng = np.random.default_rng(T * 31 + K * 7 + E)
+    announce(f"route T={T} K={K} E={E} {dtype}")
+    lab = topk_labels(T, K, E, rng)
+    sc = rng.random((T, K)).astype(np.float32)
+    _check_route(ops, lab, E, dtype, sc)
+
+
+def test_route_zipf_skew_bit_exact(ops):
+    """DeepSeek-V3 shard shape (config 4): 32768 pairs, 32 experts, Zipf(1.2), 4 empty."""
+    rng = np.random.default_rng(4)
+    counts = zipf_counts(32768, 32, 1.2, 28, rng)
+    lab = labels_from_counts(counts, rng)
+    announce("route zipf 32768x32")
+    r = _check_route(ops, lab, 32)
+    assert int((r.counts == 0).sum()) == 4
+
+
+def test_route_edge_cases(ops):
+    announce("route edge cases")
+    _check_route(ops, np.zeros((0,), np.int64), 8)  # no tokens
+    _check_route(ops, np.full((5000,), 3, np.int64), 8)  # one expert takes everything
+    rng = np.random.default_rng(9)
+    lab = rng.integers(-3, 12, 3000)  # labels outside [0, 8) sort last
+    r = _check_route(ops, lab, 8)
+    assert int(r.offsets[-1]) == int(((lab >= 0) & (lab < 8)).sum())
+
+
+def test_route_deterministic(ops):
+    rng = np.random.default_rng(10)
+    lab = torch.from_numpy(topk_labels(4096, 8, 128, rng)).to(DEV)
+    announce("route determinism")
+    a = ops.route(lab, 128).sorted_indices
+    for _ in range(3):
+        assert torch.equal(a, ops.route(lab, 128).sorted_indices)
+
+
+@pytest.mark.parametrize("T,K,E,D", [(512, 8, 128, 2048), (300, 2, 6, 64), (64, 1, 4, 7168)])
+def test_token_permute_unpermute(ops, T, K, E, D):
+    rng = np.random.default_rng(T + D)
+    tok = rand_bf16(rng, (T, D))
+    lab = topk_labels(T, K, E, rng)
+    probs = rng.random((T, K)).astype(np.float32)
+    announce(f"token_permute T={T} K={K} E={E} D={D}")
+    permuted, sidx = ops.token_permute(bf16_dev(tok), torch.from_numpy(lab).to(DEV), E)
+    ref_p, ref_s = O.permute(tok, lab, K, E)
+    np.testing.assert_array_equal(sidx.cpu().numpy(), ref_s)
+    np.testing.assert_array_equal(to_np(permuted), ref_p)
+    un = ops.token_unpermute(permuted, sidx, None, K)
+    np.testing.assert_array_equal(to_np(un), O.unpermute(ref_p, ref_s, None, K))
+    unp = ops.token_unpermute(permuted, sidx, f32_dev(probs), K)
+    assert O.max_rel_err(to_np(unp), O.unpermute(ref_p, ref_s, probs, K)) < 1e-2
+    gout = rand_bf16(rng, (T, D))
+    gp, gprobs = ops.token_unpermute_grad(bf16_dev(gout), sidx, f32_dev(probs), permuted, K, need_probs_grad=True)
+    ref_gp, ref_gprobs = O.unpermute_grad(gout, ref_s, probs, K, permuted=ref_p)
+    np.testing.assert_array_equal(to_np(gp), ref_gp)
+    assert O.max_rel_err(gprobs.cpu().numpy(), ref_gprobs) < 1e-4
+
+
+def test_unpermute_top1_round_trip(ops):
+    """NPUMoeTokenUnpermute contract (npu_permute.py:15-53): unpermute(permute(x)) == x."""
+    pkg = __import__("importlib").import_module("torchtitan-ascend_amd")
+    rng = np.random.default_rng(5)
+    T, D, E = 777, 256, 9
+    x = bf16_dev(rand_bf16(rng, (T, D))).requires_grad_(True)
+    lab = torch.from_numpy(rng.integers(0, E, T)).to(DEV)
+    announce("unpermute round trip")
+    permuted, sidx = ops.token_permute(x.detach(), lab, E)
+    permuted.requires_grad_(True)
+    back = pkg.HIPMoeTokenUnpermute.apply(permuted, sidx, x.shape)
+    assert torch.equal(back, x.detach())
+    g = torch.randn_like(back)
+    back.backward(g)
+    np.testing.assert_array_equal(to_np(permuted.grad), to_np(g)[sidx.cpu().numpy()])
+    empty = torch.empty(0, D, dtype=torch.bfloat16, device=DEV)
+    assert pkg.HIPMoeTokenUnpermute.apply(empty, sidx[:0], empty.shape).numel() == 0
+
+
+def test_gather_rows_score_before_bit_exact(ops):
+    """Dispatch with score_before_experts: bf16(float(x) * score), rounded once."""
+    rng = np.random.default_rng(6)
+    T, K, E, D = 1024, 2, 16, 512
+    x = rand_bf16(rng, (T, D))
+    lab = topk_labels(T, K, E, rng)
+    sc = rng.random((T, K)).astype(np.float32)
+    announce("gather_rows score-before")
+    r = ops.route(torch.from_numpy(lab).to(DEV), E, f32_dev(sc))
+    routed = ops.gather_rows(bf16_dev(x), r.sorted_indices, K, r.sorted_scores)
+    sidx = O.stable_order(lab, E)
+    ref = O.bf16_round(x[sidx // K] * sc.reshape(-1)[sidx][:, None])
+    np.testing.assert_array_equal(to_np(routed), ref)
+
+
+def test_regroup_permute_matches_reference_semantics(pkg):
+    """NpuTokenDispatcher._permute (npu_permute.py:63-85) with synthetic
+    (rank, expert) counts: ep=4 ranks x 8 local experts, one GPU."""
+    rng = np.random.default_rng(12)
+    ep, E_loc, D = 4, 8, 256
+    counts_group = rng.integers(0, 40, ep * E_loc)
+    counts_group[[3, 17]] = 0
+    M = int(counts_group.sum())
+    x = rand_bf16(rng, (M, D))
+    disp = pkg.HipTokenDispatcher.Config(num_experts=E_loc * ep, top_k=1).build()
+    announce("regroup permute ep=4")
+    shape, permuted, pidx, ntpe = disp._permute(bf16_dev(x), torch.from_numpy(counts_group).to(DEV), ep, E_loc)
+    ref_p, ref_s, ref_n = O.regroup_permute(x, counts_group, ep, E_loc)
+    np.testing.assert_array_equal(pidx.cpu().numpy(), ref_s)
+    np.testing.assert_array_equal(to_np(permuted), ref_p)
+    np.testing.assert_array_equal(ntpe.cpu().numpy(), ref_n)
+    back = disp._unpermute(permuted, shape, pidx)
+    np.testing.assert_array_equal(to_np(back), x)
+
+
+def test_group_labels_golden(ops):
+    g = load_golden("regroup_labels")
+    announce("group labels golden")
+    lab = ops.group_labels(torch.from_numpy(g["counts_group"]).to(DEV), int(g["num_local_experts"]), g["labels"].size + 2)
+    np.testing.assert_array_equal(lab.cpu().numpy(), O.group_labels(g["counts_group"], int(g["num_local_experts"]), g["labels"].size + 2))
+    np.testing.assert_array_equal(lab.cpu().numpy()[:-2], g["labels"])
+
+
+@pytest.mark.parametrize("name", golden_names("router_"))
+def test_router_topk_golden(ops, name):
+    g = load_golden(name)
+    func = "softmax" if "softmax" in name else "sigmoid"
+    norm = name.endswith("norm")
+    K = int(g["top_k"])
+    announce(f"router golden {name}")
+    s, i = ops.router_topk(f32_dev(g["logits"]), K, func, norm)
+    np.testing.assert_array_equal(i.cpu().numpy(), g["indices"])
+    np.testing.assert_allclose(s.cpu().numpy(), g["scores"], rtol=2e-6, atol=1e-7)
+    s, i = ops.router_topk(f32_dev(g["logits"]), K, func, False, expert_bias=f32_dev(g["bias"]))
+    np.testing.assert_array_equal(i.cpu().numpy(), g["indices_bias"])
+    np.testing.assert_allclose(s.cpu().numpy(), g["scores_bias"], rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("T,E,K,func,norm", [(8192, 128, 8, "softmax", True), (8192, 16, 1, "sigmoid", False),
+                                             (1000, 256, 8, "sigmoid", True), (33, 1024, 16, "softmax", False)])
+def test_router_topk_vs_oracle(ops, T, E, K, func, norm):
+    rng = np.random.default_rng(E + K)
+    # distinct logits with gaps >= 0.04, so no two scores are within rounding
+    logits = (np.argsort(rng.random((T, E)), axis=1) * 0.05 - E * 0.025).astype(np.float32)
+    logits += rng.uniform(-0.005, 0.005, (T, E)).astype(np.float32)
+    announce(f"router T={T} E={E} K={K} {func}")
+    s, i = ops.router_topk(f32_dev(logits), K, func, norm, route_scale=1.5)
+    rs, ri = O.router_topk(logits, K, func, norm, route_scale=1.5)
+    np.testing.assert_array_equal(i.cpu().numpy(), ri)
+    np.testing.assert_allclose(s.cpu().numpy(), rs, rtol=1e-5, atol=1e-7)
+
+
+def test_router_ties(ops):
+    logits = np.array([[1.0, 3.0, 3.0, 0.0, 3.0], [2.0, 2.0, 2.0, 2.0, 2.0]], np.float32)
+    announce("router ties")
+    _, i = ops.router_topk(f32_dev(logits), 3, "sigmoid")
+    np.testing.assert_array_equal(i.cpu().numpy(), [[1, 2, 4], [0, 1, 2]])

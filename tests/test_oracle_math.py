@@ -1,0 +1,142 @@
+"""Pins the oracle's floating-point functions (CPU only).
+
+Checks: torch._grouped_mm bf16 chain (the reference's own op sequence,
+npu_gmm.py:29-38), torch autograd of an fp32 restatement (index_add form of
+qwen3_5/model.py:703-735), torch softmax/sigmoid/topk, torch bf16 casts,
+and planted mistakes that the checks must catch.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import golden_names, load_golden
+from oracle import moe_oracle as O
+
+
+def _limit(g):
+    v = float(g["limit"])
+    return None if np.isnan(v) else v
+
+
+def test_bf16_round_matches_torch():
+    g = load_golden("bf16_round")
+    np.testing.assert_array_equal(O.bf16_round(g["values"]), g["rounded"])
+
+
+@pytest.mark.parametrize("name", golden_names("experts_"))
+def test_experts_forward_matches_torch_grouped_mm(name):
+    g = load_golden(name)
+    y, h, a = O.experts_forward(g["x"], g["w13"], g["w2"], g["counts"], _limit(g), round_intermediates=True)
+    M = int(g["counts"].sum())
+    # h: same products, same rounding point; accumulation order may differ by an ulp
+    assert O.max_rel_err(h[:M], O.bf16_round(g["h_f32"])) < 1e-2
+    L = _limit(g)
+    if L is not None:  # the reference keeps the clamped h (npu_gmm.py:33-36)
+        H = h.shape[1] // 2
+        hc = np.concatenate([np.minimum(h[:, :H], L), np.clip(h[:, H:], -L, L)], axis=1)
+        assert O.max_rel_err(hc[:M], g["h_bf16"]) < 1e-2
+    assert O.max_rel_err(a[:M], g["a_bf16"]) < 2e-2
+    assert O.max_rel_err(y[:M], g["y_bf16"]) < 2e-2
+    # the unclamped pre-activation agrees with the fp32 per-expert loop
+    yf, hf, _ = O.experts_forward(g["x"], g["w13"], g["w2"], g["counts"], None, round_intermediates=False)
+    assert O.max_rel_err(hf[:M], g["h_f32"]) < 1e-5
+
+
+@pytest.mark.parametrize("name", golden_names("layer_"))
+def test_moe_forward_matches_autograd_golden(name):
+    g = load_golden(name)
+    E = int(g["num_experts"])
+    out = O.moe_forward(g["x"], g["scores"], g["idx"], g["w13"], g["w2"], E, bool(g["score_before"]),
+                        _limit(g), round_intermediates=False)
+    assert O.max_rel_err(out, g["out"]) < 1e-5
+
+
+@pytest.mark.parametrize("name", golden_names("layer_"))
+def test_moe_backward_matches_autograd_golden(name):
+    g = load_golden(name)
+    E = int(g["num_experts"])
+    grads = O.moe_backward(g["x"], g["scores"], g["idx"], g["w13"], g["w2"], E, bool(g["score_before"]),
+                           g["dout"], _limit(g))
+    for k in ("dx", "dw13", "dw2", "dscores"):
+        assert O.max_rel_err(grads[k], g[k]) < 1e-4, k
+
+
+def test_moe_forward_brute_token_loop():
+    """Per-token loop in the form of qwen3_5/model.py:703-735 (weights applied
+    after the expert, summed with index_add) for the score-after layout."""
+    rng = np.random.default_rng(11)
+    T, K, E, D, H = 10, 2, 5, 16, 8
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    w13 = (rng.standard_normal((E, 2 * H, D)) * 0.3).astype(np.float32)
+    w2 = (rng.standard_normal((E, D, H)) * 0.3).astype(np.float32)
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(T)])
+    sc = rng.random((T, K)).astype(np.float32)
+    ref = np.zeros((T, D))
+    for t in range(T):
+        for k in range(K):
+            e = idx[t, k]
+            h = w13[e].astype(np.float64) @ x[t]
+            a = h[:H] / (1 + np.exp(-h[:H])) * h[H:]
+            ref[t] += sc[t, k] * (w2[e].astype(np.float64) @ a)
+    out = O.moe_forward(x, sc, idx, w13, w2, E, False, None, round_intermediates=False)
+    assert O.max_rel_err(out, ref) < 1e-5
+
+
+def test_finite_difference_dscores():
+    """Central differences of the fp64-evaluated forward w.r.t. one score."""
+    rng = np.random.default_rng(12)
+    T, K, E, D, H = 6, 2, 3, 8, 4
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    w13 = (rng.standard_normal((E, 2 * H, D)) * 0.5).astype(np.float32)
+    w2 = (rng.standard_normal((E, D, H)) * 0.5).astype(np.float32)
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(T)])
+    sc = (rng.random((T, K)) + 0.5).astype(np.float32)
+    dout = rng.standard_normal((T, D)).astype(np.float32)
+    for before in (False, True):
+        grads = O.moe_backward(x, sc, idx, w13, w2, E, before, dout)
+        for (t, k) in ((0, 0), (3, 1)):
+            eps = 1e-2
+            sp, sm = sc.copy(), sc.copy()
+            sp[t, k] += eps
+            sm[t, k] -= eps
+            fp = O.moe_forward(x, sp, idx, w13, w2, E, before, None, round_intermediates=False)
+            fm = O.moe_forward(x, sm, idx, w13, w2, E, before, None, round_intermediates=False)
+            fd = ((fp.astype(np.float64) - fm) * dout).sum() / (2 * eps)
+            assert abs(fd - grads["dscores"][t, k]) < 2e-3 * max(1.0, abs(fd)), (before, t, k)
+
+
+@pytest.mark.parametrize("name", golden_names("router_"))
+def test_router_topk_matches_torch(name):
+    g = load_golden(name)
+    func = "softmax" if "softmax" in name else "sigmoid"
+    norm = name.endswith("norm")
+    K = int(g["top_k"])
+    s, i = O.router_topk(g["logits"], K, func, norm)
+    np.testing.assert_array_equal(i, g["indices"])
+    np.testing.assert_allclose(s, g["scores"], rtol=1e-6, atol=1e-7)
+    s, i = O.router_topk(g["logits"], K, func, False, expert_bias=g["bias"])
+    np.testing.assert_array_equal(i, g["indices_bias"])
+    np.testing.assert_allclose(s, g["scores_bias"], rtol=1e-6, atol=1e-7)
+
+
+def test_router_ties_prefer_lower_expert():
+    logits = np.array([[1.0, 3.0, 3.0, 0.0, 3.0], [2.0, 2.0, 2.0, 2.0, 2.0]], np.float32)
+    _, i = O.router_topk(logits, 3, "sigmoid")
+    np.testing.assert_array_equal(i, [[1, 2, 4], [0, 1, 2]])
+
+
+def test_planted_gate_up_swap_is_caught():
+    """Swapping gate and up halves (a plausible layout mistake) fails the golden."""
+    g = load_golden("experts_nolimit")
+    H = g["w13"].shape[1] // 2
+    w13_swapped = np.concatenate([g["w13"][:, H:], g["w13"][:, :H]], axis=1)
+    y, _, _ = O.experts_forward(g["x"], w13_swapped, g["w2"], g["counts"], None)
+    assert O.max_rel_err(y, g["y_bf16"]) > 0.1
+
+
+def test_planted_missing_score_is_caught():
+    g = load_golden("layer_k2_after")
+    out = O.moe_forward(g["x"], np.ones_like(g["scores"]), g["idx"], g["w13"], g["w2"], int(g["num_experts"]),
+                        False, None, round_intermediates=False)
+    assert O.max_rel_err(out, g["out"]) > 0.1

@@ -1,0 +1,437 @@
+// extern "C" entry points of libttamd_moe.so (declared in include/ttamd_moe.h).
+//
+// This layer owns argument validation: every size, alignment and range the
+// kernels rely on is checked here, on the host, before anything is launched.
+// A rejected call returns TTAMD_EINVAL and launches nothing.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/ttamd_moe.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_hip(hipError_t err, const char* what) {
+  if (err != hipSuccess) return fail(TTAMD_ERUNTIME, "%s: %s", what, hipGetErrorString(err));
+  return TTAMD_OK;
+}
+
+constexpr int64_t kI32Max = 2147483647;
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+#define REQUIRE(cond, ...)                        \
+  do {                                            \
+    if (!(cond)) return fail(TTAMD_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+// Rows of `hidden` bf16 moved as 16-byte chunks.
+int check_rows(const char* fn, const char* name, const void* p, int64_t rows, int64_t hidden) {
+  if (rows > 0 && p == nullptr) return fail(TTAMD_EINVAL, "%s: %s is null", fn, name);
+  if (rows > 0 && !aligned16(p))
+    return fail(TTAMD_EINVAL, "%s: %s must be 16-byte aligned", fn, name);
+  // 16-byte chunk indices stay below 2^30 so grid-stride arithmetic never
+  // approaches the int32 range.
+  if (rows * (hidden / 8) > (int64_t(1) << 30))
+    return fail(TTAMD_EINVAL, "%s: %s has too many elements (%lld x %lld)", fn, name,
+                (long long)rows, (long long)hidden);
+  return TTAMD_OK;
+}
+
+int check_hidden(const char* fn, int64_t hidden) {
+  if (hidden <= 0 || hidden % 8 != 0)
+    return fail(TTAMD_EINVAL, "%s: hidden must be a positive multiple of 8 (got %lld)", fn,
+                (long long)hidden);
+  return TTAMD_OK;
+}
+
+int check_gemm_common(const char* fn, const int32_t* offs, int64_t M, int E) {
+  REQUIRE(offs != nullptr, "%s: offs is null", fn);
+  REQUIRE(E >= 1 && E <= 1024, "%s: num_experts must be in [1, 1024] (got %d)", fn, E);
+  REQUIRE(M >= 0 && M <= (1 << 28), "%s: num_rows out of range (%lld)", fn, (long long)M);
+  return TTAMD_OK;
+}
+
+int check_dim(const char* fn, const char* name, int64_t v, int mult) {
+  if (v <= 0 || v % mult != 0 || v > (1 << 20))
+    return fail(TTAMD_EINVAL, "%s: %s must be a positive multiple of %d (got %lld)", fn, name,
+                mult, (long long)v);
+  return TTAMD_OK;
+}
+
+int check_ws(const char* fn, const void* ws, size_t have, size_t need) {
+  if (need > 0 && (ws == nullptr || have < need))
+    return fail(TTAMD_EINVAL, "%s: workspace too small (%zu bytes, need %zu)", fn, have, need);
+  if (ws != nullptr && !aligned16(ws)) return fail(TTAMD_EINVAL, "%s: workspace must be 16-byte aligned", fn);
+  return TTAMD_OK;
+}
+
+#define TRY(expr)            \
+  do {                       \
+    int _rc = (expr);        \
+    if (_rc != TTAMD_OK) return _rc; \
+  } while (0)
+
+}  // namespace
+
+extern "C" {
+
+int ttamd_abi_version(void) { return TTAMD_ABI_VERSION; }
+
+const char* ttamd_last_error(void) { return g_last_error.c_str(); }
+
+int ttamd_router_topk(const float* logits, const float* expert_bias, int64_t num_tokens,
+                      int num_experts, int topk, int score_func, int renorm, float renorm_eps,
+                      float route_scale, float* top_scores, int64_t* top_indices, void* stream) {
+  const char* fn = "ttamd_router_topk";
+  REQUIRE(num_tokens >= 0 && num_tokens * (int64_t)num_experts <= kI32Max * 4LL,
+          "%s: num_tokens out of range", fn);
+  REQUIRE(num_experts >= 1 && num_experts <= 1024, "%s: num_experts must be in [1, 1024]", fn);
+  REQUIRE(topk >= 1 && topk <= 16 && topk <= num_experts, "%s: topk must be in [1, min(16, E)]",
+          fn);
+  REQUIRE(score_func == TTAMD_SCORE_SOFTMAX || score_func == TTAMD_SCORE_SIGMOID,
+          "%s: unknown score_func %d", fn, score_func);
+  REQUIRE(num_tokens <= kI32Max, "%s: num_tokens too large", fn);
+  if (num_tokens > 0)
+    REQUIRE(logits && top_scores && top_indices, "%s: null pointer argument", fn);
+  return check_hip(ttamd::launch_router_topk(logits, expert_bias, (int)num_tokens, num_experts,
+                                             topk, score_func, renorm, renorm_eps, route_scale,
+                                             top_scores, top_indices, (hipStream_t)stream),
+                   fn);
+}
+
+size_t ttamd_route_workspace_bytes(int64_t num_flat, int num_experts) {
+  if (num_flat < 0 || num_experts < 1) return 0;
+  return ttamd::route_workspace_bytes(num_flat, num_experts);
+}
+
+static int route_checks(const char* fn, const void* labels, int64_t M, int E, const float* scores,
+                        const int32_t* sorted, const float* sorted_scores, const void* ws,
+                        size_t ws_bytes) {
+  REQUIRE(M >= 0 && M <= (1 << 28), "%s: number of labels out of range (%lld)", fn,
+          (long long)M);
+  REQUIRE(E >= 1 && E <= 1024, "%s: num_experts must be in [1, 1024] (got %d)", fn, E);
+  if (M > 0) REQUIRE(labels && sorted, "%s: null pointer argument", fn);
+  REQUIRE((scores == nullptr) == (sorted_scores == nullptr),
+          "%s: scores and sorted_scores must be given together", fn);
+  TRY(check_ws(fn, ws, ws_bytes, ttamd::route_workspace_bytes(M, E)));
+  return TTAMD_OK;
+}
+
+int ttamd_moe_route(const void* labels, int labels_are_int64, int64_t num_flat, int num_experts,
+                    const float* scores, int32_t* counts, int32_t* offsets,
+                    int32_t* sorted_indices, int32_t* inverse, float* sorted_scores,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "ttamd_moe_route";
+  TRY(route_checks(fn, labels, num_flat, num_experts, scores, sorted_indices, sorted_scores,
+                   workspace, workspace_bytes));
+  return check_hip(ttamd::launch_route(labels, labels_are_int64 != 0, (int)num_flat, num_experts,
+                                       scores, counts, offsets, sorted_indices, inverse,
+                                       sorted_scores, workspace, (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_moe_gather_rows(const void* in, const int32_t* src_index, const float* row_scale,
+                          int64_t num_in_rows, int64_t num_out_rows, int64_t hidden, int topk,
+                          void* out, void* stream) {
+  const char* fn = "ttamd_moe_gather_rows";
+  TRY(check_hidden(fn, hidden));
+  REQUIRE(topk >= 1, "%s: topk must be >= 1", fn);
+  REQUIRE(num_in_rows >= 0 && num_out_rows >= 0, "%s: negative row count", fn);
+  REQUIRE(num_out_rows == 0 || num_in_rows > 0, "%s: no input rows to gather from", fn);
+  REQUIRE(num_in_rows * topk <= kI32Max, "%s: too many rows", fn);
+  TRY(check_rows(fn, "in", in, num_in_rows, hidden));
+  TRY(check_rows(fn, "out", out, num_out_rows, hidden));
+  if (num_out_rows > 0) REQUIRE(src_index != nullptr, "%s: src_index is null", fn);
+  return check_hip(ttamd::launch_gather_rows(in, src_index, row_scale, false, (int)num_in_rows,
+                                             (int)(num_in_rows * topk), (int)num_out_rows,
+                                             (int)hidden, topk, out, (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_moe_token_permute(const void* tokens, const void* labels, int labels_are_int64,
+                            int64_t num_tokens, int64_t hidden, int topk, int num_experts,
+                            void* permuted, int32_t* sorted_indices, int32_t* counts,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "ttamd_moe_token_permute";
+  TRY(check_hidden(fn, hidden));
+  REQUIRE(topk >= 1, "%s: topk must be >= 1", fn);
+  REQUIRE(num_tokens >= 0, "%s: negative num_tokens", fn);
+  const int64_t M = num_tokens * topk;
+  TRY(route_checks(fn, labels, M, num_experts, nullptr, sorted_indices, nullptr, workspace,
+                   workspace_bytes));
+  TRY(check_rows(fn, "tokens", tokens, num_tokens, hidden));
+  TRY(check_rows(fn, "permuted", permuted, M, hidden));
+  hipStream_t s = (hipStream_t)stream;
+  TRY(check_hip(ttamd::launch_route(labels, labels_are_int64 != 0, (int)M, num_experts, nullptr,
+                                    counts, nullptr, sorted_indices, nullptr, nullptr, workspace,
+                                    s),
+                fn));
+  return check_hip(ttamd::launch_gather_rows(tokens, sorted_indices, nullptr, false,
+                                             (int)num_tokens, (int)M, (int)M, (int)hidden, topk,
+                                             permuted, s),
+                   fn);
+}
+
+size_t ttamd_unpermute_workspace_bytes(int64_t num_tokens, int topk) {
+  if (num_tokens < 0 || topk < 1) return 0;
+  return (size_t)(num_tokens * topk) * sizeof(int32_t) + 256;
+}
+
+int ttamd_moe_token_unpermute(const void* permuted, const int32_t* sorted_indices,
+                              const float* probs, int64_t num_tokens, int64_t hidden, int topk,
+                              void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "ttamd_moe_token_unpermute";
+  TRY(check_hidden(fn, hidden));
+  REQUIRE(topk >= 1, "%s: topk must be >= 1", fn);
+  REQUIRE(num_tokens >= 0, "%s: negative num_tokens", fn);
+  const int64_t M = num_tokens * topk;
+  TRY(check_rows(fn, "permuted", permuted, M, hidden));
+  TRY(check_rows(fn, "out", out, num_tokens, hidden));
+  if (M > 0) REQUIRE(sorted_indices != nullptr, "%s: sorted_indices is null", fn);
+  TRY(check_ws(fn, workspace, workspace_bytes, ttamd_unpermute_workspace_bytes(num_tokens, topk)));
+  hipStream_t s = (hipStream_t)stream;
+  int32_t* inv = (int32_t*)workspace;
+  TRY(check_hip(ttamd::launch_invert_perm(sorted_indices, (int)M, inv, s), fn));
+  return check_hip(ttamd::launch_combine(permuted, inv, probs, (int)num_tokens, topk, (int)hidden,
+                                         out, s),
+                   fn);
+}
+
+int ttamd_moe_combine(const void* permuted, const int32_t* inverse, const float* probs,
+                      int64_t num_tokens, int64_t hidden, int topk, void* out, void* stream) {
+  const char* fn = "ttamd_moe_combine";
+  TRY(check_hidden(fn, hidden));
+  REQUIRE(topk >= 1, "%s: topk must be >= 1", fn);
+  REQUIRE(num_tokens >= 0, "%s: negative num_tokens", fn);
+  const int64_t M = num_tokens * topk;
+  TRY(check_rows(fn, "permuted", permuted, M, hidden));
+  TRY(check_rows(fn, "out", out, num_tokens, hidden));
+  if (M > 0) REQUIRE(inverse != nullptr, "%s: inverse is null", fn);
+  return check_hip(ttamd::launch_combine(permuted, inverse, probs, (int)num_tokens, topk,
+                                         (int)hidden, out, (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_moe_sum_topk(const void* in, int64_t num_tokens, int64_t hidden, int topk, void* out,
+                       void* stream) {
+  const char* fn = "ttamd_moe_sum_topk";
+  TRY(check_hidden(fn, hidden));
+  REQUIRE(topk >= 1, "%s: topk must be >= 1", fn);
+  REQUIRE(num_tokens >= 0, "%s: negative num_tokens", fn);
+  TRY(check_rows(fn, "in", in, num_tokens * topk, hidden));
+  TRY(check_rows(fn, "out", out, num_tokens, hidden));
+  return check_hip(ttamd::launch_combine(in, nullptr, nullptr, (int)num_tokens, topk, (int)hidden,
+                                         out, (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_moe_token_unpermute_grad(const void* grad_out, const int32_t* sorted_indices,
+                                   const float* probs, const void* permuted, int64_t num_tokens,
+                                   int64_t hidden, int topk, void* grad_permuted,
+                                   float* grad_probs, void* stream) {
+  const char* fn = "ttamd_moe_token_unpermute_grad";
+  TRY(check_hidden(fn, hidden));
+  REQUIRE(topk >= 1, "%s: topk must be >= 1", fn);
+  REQUIRE(num_tokens >= 0, "%s: negative num_tokens", fn);
+  const int64_t M = num_tokens * topk;
+  TRY(check_rows(fn, "grad_out", grad_out, num_tokens, hidden));
+  TRY(check_rows(fn, "grad_permuted", grad_permuted, M, hidden));
+  if (M > 0) REQUIRE(sorted_indices != nullptr, "%s: sorted_indices is null", fn);
+  if (grad_probs) {
+    REQUIRE(probs != nullptr && permuted != nullptr,
+            "%s: grad_probs needs probs and permuted", fn);
+    TRY(check_rows(fn, "permuted", permuted, M, hidden));
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (M == 0) return TTAMD_OK;
+  TRY(check_hip(ttamd::launch_gather_rows(grad_out, sorted_indices, probs, true, (int)num_tokens,
+                                          (int)M, (int)M, (int)hidden, topk, grad_permuted, s),
+                fn));
+  if (grad_probs)
+    TRY(check_hip(ttamd::launch_rowdot(permuted, grad_out, sorted_indices, topk, true, (int)M,
+                                       (int)num_tokens, (int)M, (int)hidden, grad_probs, s),
+                  fn));
+  return TTAMD_OK;
+}
+
+int ttamd_moe_rowdot(const void* a, const void* b, const int32_t* b_index, int b_div,
+                     int out_by_index, int64_t num_rows, int64_t num_b_rows, int64_t hidden,
+                     float* out, void* stream) {
+  const char* fn = "ttamd_moe_rowdot";
+  TRY(check_hidden(fn, hidden));
+  REQUIRE(b_div >= 1, "%s: b_div must be >= 1", fn);
+  REQUIRE(num_rows >= 0 && num_b_rows >= 0, "%s: negative row count", fn);
+  REQUIRE(num_rows == 0 || num_b_rows > 0, "%s: b has no rows", fn);
+  TRY(check_rows(fn, "a", a, num_rows, hidden));
+  TRY(check_rows(fn, "b", b, num_b_rows, hidden));
+  if (num_rows > 0) REQUIRE(out != nullptr, "%s: out is null", fn);
+  REQUIRE(!out_by_index || b_index != nullptr, "%s: out_by_index needs b_index", fn);
+  REQUIRE(num_b_rows * (int64_t)b_div <= kI32Max, "%s: too many rows", fn);
+  return check_hip(ttamd::launch_rowdot(a, b, b_index, b_div, out_by_index != 0, (int)num_rows,
+                                        (int)num_b_rows, (int)num_rows, (int)hidden, out,
+                                        (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_moe_group_labels(const int32_t* counts_group, int num_groups, int num_local_experts,
+                           int64_t num_rows, int32_t* labels, void* stream) {
+  const char* fn = "ttamd_moe_group_labels";
+  REQUIRE(num_groups >= 1 && num_groups <= 8192, "%s: num_groups must be in [1, 8192]", fn);
+  REQUIRE(num_local_experts >= 1 && num_groups % num_local_experts == 0,
+          "%s: num_groups must be a multiple of num_local_experts", fn);
+  REQUIRE(num_rows >= 0 && num_rows <= kI32Max, "%s: num_rows out of range", fn);
+  REQUIRE(counts_group != nullptr, "%s: counts_group is null", fn);
+  if (num_rows > 0) REQUIRE(labels != nullptr, "%s: labels is null", fn);
+  return check_hip(ttamd::launch_group_labels(counts_group, num_groups, num_local_experts,
+                                              (int)num_rows, labels, (hipStream_t)stream),
+                   fn);
+}
+
+size_t ttamd_gemm_workspace_bytes(int64_t num_rows, int num_experts) {
+  if (num_rows < 0 || num_experts < 1) return 0;
+  return ttamd::gemm_workspace_bytes(num_rows, num_experts);
+}
+
+int ttamd_grouped_mm(const void* x, const void* w, const int32_t* offs, int64_t num_rows,
+                     int num_experts, int64_t n, int64_t k, void* out, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  const char* fn = "ttamd_grouped_mm";
+  TRY(check_gemm_common(fn, offs, num_rows, num_experts));
+  TRY(check_dim(fn, "n", n, 128));
+  TRY(check_dim(fn, "k", k, 64));
+  REQUIRE(w && aligned16(w), "%s: w must be non-null and 16-byte aligned", fn);
+  TRY(check_rows(fn, "x", x, num_rows, k));
+  TRY(check_rows(fn, "out", out, num_rows, n));
+  TRY(check_ws(fn, workspace, workspace_bytes, ttamd::gemm_workspace_bytes(num_rows, num_experts)));
+  if (num_rows == 0) return TTAMD_OK;
+  return check_hip(ttamd::launch_grouped_mm(x, w, offs, (int)num_rows, num_experts, (int)n, (int)k,
+                                            out, workspace, (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_grouped_mm_swiglu(const void* x, const void* w13, const int32_t* offs,
+                            int64_t num_rows, int num_experts, int64_t hidden, int64_t dim,
+                            float swiglu_limit, void* a_out, void* h_out, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  const char* fn = "ttamd_grouped_mm_swiglu";
+  TRY(check_gemm_common(fn, offs, num_rows, num_experts));
+  TRY(check_dim(fn, "hidden", hidden, 64));
+  TRY(check_dim(fn, "dim", dim, 64));
+  REQUIRE(std::isnan(swiglu_limit) || swiglu_limit >= 0.f,
+          "%s: swiglu_limit must be NaN (no clamp) or >= 0", fn);
+  REQUIRE(w13 && aligned16(w13), "%s: w13 must be non-null and 16-byte aligned", fn);
+  TRY(check_rows(fn, "x", x, num_rows, dim));
+  TRY(check_rows(fn, "a_out", a_out, num_rows, hidden));
+  if (h_out) TRY(check_rows(fn, "h_out", h_out, num_rows, 2 * hidden));
+  TRY(check_ws(fn, workspace, workspace_bytes, ttamd::gemm_workspace_bytes(num_rows, num_experts)));
+  if (num_rows == 0) return TTAMD_OK;
+  return check_hip(ttamd::launch_grouped_mm_swiglu(x, w13, offs, (int)num_rows, num_experts,
+                                                   (int)hidden, (int)dim, swiglu_limit, a_out,
+                                                   h_out, workspace, (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_grouped_mm_unpermute(const void* a, const void* w2, const int32_t* offs,
+                               int64_t num_rows, int num_experts, int64_t dim, int64_t hidden,
+                               const float* row_scale, const int32_t* dest, int64_t num_dest_rows,
+                               void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "ttamd_grouped_mm_unpermute";
+  TRY(check_gemm_common(fn, offs, num_rows, num_experts));
+  TRY(check_dim(fn, "dim", dim, 128));
+  TRY(check_dim(fn, "hidden", hidden, 64));
+  REQUIRE(w2 && aligned16(w2), "%s: w2 must be non-null and 16-byte aligned", fn);
+  TRY(check_rows(fn, "a", a, num_rows, hidden));
+  if (dest == nullptr)
+    REQUIRE(num_dest_rows >= num_rows, "%s: out needs num_rows rows when dest is null", fn);
+  REQUIRE(num_dest_rows >= 0, "%s: negative num_dest_rows", fn);
+  REQUIRE(num_rows == 0 || num_dest_rows > 0, "%s: out has no rows", fn);
+  TRY(check_rows(fn, "out", out, num_dest_rows, dim));
+  TRY(check_ws(fn, workspace, workspace_bytes, ttamd::gemm_workspace_bytes(num_rows, num_experts)));
+  if (num_rows == 0) return TTAMD_OK;
+  return check_hip(ttamd::launch_grouped_mm_unpermute(a, w2, offs, (int)num_rows, num_experts,
+                                                      (int)dim, (int)hidden, row_scale, dest,
+                                                      (int)num_dest_rows, out, workspace,
+                                                      (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_grouped_mm_dgrad(const void* dy, const void* w, const int32_t* offs, int64_t num_rows,
+                           int num_experts, int64_t n, int64_t k, void* dx, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  const char* fn = "ttamd_grouped_mm_dgrad";
+  TRY(check_gemm_common(fn, offs, num_rows, num_experts));
+  TRY(check_dim(fn, "n", n, 64));
+  TRY(check_dim(fn, "k", k, 128));
+  REQUIRE(w && aligned16(w), "%s: w must be non-null and 16-byte aligned", fn);
+  TRY(check_rows(fn, "dy", dy, num_rows, n));
+  TRY(check_rows(fn, "dx", dx, num_rows, k));
+  TRY(check_ws(fn, workspace, workspace_bytes, ttamd::gemm_workspace_bytes(num_rows, num_experts)));
+  if (num_rows == 0) return TTAMD_OK;
+  return check_hip(ttamd::launch_grouped_mm_dgrad(dy, w, offs, (int)num_rows, num_experts, (int)n,
+                                                  (int)k, dx, workspace, (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_grouped_mm_dgrad_swiglu(const void* dy, const void* w2, const void* h,
+                                  const int32_t* offs, int64_t num_rows, int num_experts,
+                                  int64_t dim, int64_t hidden, float swiglu_limit, void* dh,
+                                  void* a_out, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  const char* fn = "ttamd_grouped_mm_dgrad_swiglu";
+  TRY(check_gemm_common(fn, offs, num_rows, num_experts));
+  TRY(check_dim(fn, "dim", dim, 64));
+  TRY(check_dim(fn, "hidden", hidden, 128));
+  REQUIRE(std::isnan(swiglu_limit) || swiglu_limit >= 0.f,
+          "%s: swiglu_limit must be NaN (no clamp) or >= 0", fn);
+  REQUIRE(w2 && aligned16(w2), "%s: w2 must be non-null and 16-byte aligned", fn);
+  TRY(check_rows(fn, "dy", dy, num_rows, dim));
+  TRY(check_rows(fn, "h", h, num_rows, 2 * hidden));
+  TRY(check_rows(fn, "dh", dh, num_rows, 2 * hidden));
+  if (a_out) TRY(check_rows(fn, "a_out", a_out, num_rows, hidden));
+  TRY(check_ws(fn, workspace, workspace_bytes, ttamd::gemm_workspace_bytes(num_rows, num_experts)));
+  if (num_rows == 0) return TTAMD_OK;
+  return check_hip(ttamd::launch_grouped_mm_dgrad_swiglu(dy, w2, h, offs, (int)num_rows,
+                                                         num_experts, (int)dim, (int)hidden,
+                                                         swiglu_limit, dh, a_out, workspace,
+                                                         (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_grouped_mm_wgrad(const void* dy, const void* x, const int32_t* offs, int64_t num_rows,
+                           int num_experts, int64_t n, int64_t k, void* dw, int dw_is_fp32,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "ttamd_grouped_mm_wgrad";
+  (void)workspace;
+  (void)workspace_bytes;
+  TRY(check_gemm_common(fn, offs, num_rows, num_experts));
+  TRY(check_dim(fn, "n", n, 128));
+  TRY(check_dim(fn, "k", k, 128));
+  TRY(check_rows(fn, "dy", dy, num_rows, n));
+  TRY(check_rows(fn, "x", x, num_rows, k));
+  REQUIRE(dw && aligned16(dw), "%s: dw must be non-null and 16-byte aligned", fn);
+  REQUIRE((int64_t)num_experts * n * k <= (int64_t)1 << 40, "%s: dw too large", fn);
+  REQUIRE((int64_t)num_experts * (n / 128) * (k / 128) <= kI32Max, "%s: too many tiles", fn);
+  return check_hip(ttamd::launch_grouped_mm_wgrad(dy, x, offs, (int)num_rows, num_experts, (int)n,
+                                                  (int)k, dw, dw_is_fp32 != 0,
+                                                  (hipStream_t)stream),
+                   fn);
+}
+
+}  // extern "C"

@@ -1,0 +1,52 @@
+// Host-side launchers of the device kernels (internal to libttamd_moe.so).
+// All sizes have been validated by the C ABI layer before these are called.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ttamd {
+
+// routing.hip
+size_t route_workspace_bytes(int64_t M, int E);
+hipError_t launch_route(const void* labels, bool is64, int M, int E, const float* scores,
+                        int* counts, int* offsets, int* sorted_idx, int* inverse,
+                        float* sorted_scores, void* ws, hipStream_t stream);
+hipError_t launch_gather_rows(const void* in, const int* src, const float* scale,
+                              bool scale_by_src, int n_in, int n_src_max, int rows, int hidden,
+                              int div, void* out, hipStream_t stream);
+hipError_t launch_invert_perm(const int* sorted, int M, int* inv, hipStream_t stream);
+hipError_t launch_combine(const void* in, const int* inverse, const float* probs, int T,
+                          int topk, int hidden, void* out, hipStream_t stream);
+hipError_t launch_rowdot(const void* a, const void* b, const int* bidx, int bdiv,
+                         bool out_by_bidx, int rows, int n_b, int n_out, int hidden, float* out,
+                         hipStream_t stream);
+hipError_t launch_group_labels(const int* counts_group, int G, int E_loc, int rows, int* labels,
+                               hipStream_t stream);
+hipError_t launch_router_topk(const float* logits, const float* bias, int T, int E, int K,
+                              int score_func, int renorm, float renorm_eps, float route_scale,
+                              float* top_scores, int64_t* top_idx, hipStream_t stream);
+
+// gemm.hip
+int gemm_max_qtiles(int M, int E);
+size_t gemm_workspace_bytes(int64_t M, int E);
+hipError_t launch_grouped_mm(const void* x, const void* w, const int* offs, int M, int E, int N,
+                             int K, void* out, void* ws, hipStream_t stream);
+hipError_t launch_grouped_mm_swiglu(const void* x, const void* w13, const int* offs, int M,
+                                    int E, int H, int D, float limit, void* a_out, void* h_out,
+                                    void* ws, hipStream_t stream);
+hipError_t launch_grouped_mm_unpermute(const void* act, const void* w2, const int* offs, int M,
+                                       int E, int D, int H, const float* row_scale,
+                                       const int* dest, int n_dest, void* out, void* ws,
+                                       hipStream_t stream);
+hipError_t launch_grouped_mm_dgrad(const void* dy, const void* w, const int* offs, int M, int E,
+                                   int N, int K, void* dx, void* ws, hipStream_t stream);
+hipError_t launch_grouped_mm_dgrad_swiglu(const void* dy, const void* w2, const void* h,
+                                          const int* offs, int M, int E, int D, int H,
+                                          float limit, void* dh, void* a_out, void* ws,
+                                          hipStream_t stream);
+hipError_t launch_grouped_mm_wgrad(const void* dy, const void* x, const int* offs, int M, int E,
+                                   int N, int K, void* dw, bool fp32, hipStream_t stream);
+
+}  // namespace ttamd

@@ -1,0 +1,559 @@
+// Routing kernels of the MoE expert path on MI355X (gfx950):
+//   router top-k, per-expert histogram, stable counting sort (wavefront
+//   ballot match + LDS wave prefixes), row gather (permute), gather-reduce
+//   (unpermute / combine) and row dot products (routing-score gradients).
+//
+// Semantics follow the reference path:
+//   * histogram + stable argsort of the flat expert labels: upstream
+//     TorchTitan dispatch, reached from
+//     torchtitanturbo/models/common/npu_gmm.py:106-108, and the index half of
+//     torch_npu.npu_moe_token_permute (npu_permute.py:74-76);
+//   * row gather = npu_moe_token_permute's row half / upstream dispatch's
+//     `x[token_indices]` (+ fp32 score multiply when score_before_experts);
+//   * gather-reduce = _npu_moe_token_unpermute_with_routing_map
+//     (npu_permute.py:23-30) and upstream combine;
+//   * unpermute grad = npu_moe_token_unpermute_with_routing_map_grad
+//     (npu_permute.py:41-50).
+// Every kernel that indexes memory with device-resident indices clamps them
+// into the valid range, so a corrupt index array yields wrong values, never
+// an out-of-bounds access.
+#include "common.h"
+#include "kernels.h"
+
+namespace ttamd {
+
+// ---------------------------------------------------------------------------
+// Stable counting sort.
+//
+// The flat label array is cut into chunks of kRouteChunk elements, one per
+// workgroup.  Bucket E collects labels outside [0, E) so that every position
+// of the output permutation is written exactly once.
+//   pass 1 (hist): per-chunk bucket counts, stored bucket-major
+//                  hist[b * nchunks + chunk];
+//   pass 2 (scan): one workgroup turns hist into an exclusive prefix sum over
+//                  that bucket-major order, which is exactly the first output
+//                  position of (bucket b, chunk c);
+//   pass 3 (rank): each wave owns 256 consecutive elements, finds equal
+//                  labels among its 64 lanes with log2(E+1) ballots, and adds
+//                  its wave-local rank to a per-wave running base kept in LDS.
+// ---------------------------------------------------------------------------
+constexpr int kRouteThreads = 256;
+constexpr int kRouteWaves = kRouteThreads / kWave;
+constexpr int kRoutePerWave = 256;
+constexpr int kRouteChunk = kRouteWaves * kRoutePerWave;  // 1024
+constexpr int kScanThreads = 1024;
+
+template <typename IdxT>
+__device__ __forceinline__ int bucket_of(const IdxT* labels, int i, int E) {
+  const IdxT v = labels[i];
+  return (v >= 0 && v < (IdxT)E) ? (int)v : E;
+}
+
+template <typename IdxT>
+__global__ __launch_bounds__(kRouteThreads) void route_hist_kernel(
+    const IdxT* __restrict__ labels, int M, int E, int nchunks,
+    int* __restrict__ hist) {
+  extern __shared__ int sh_hist[];  // E + 1
+  for (int b = threadIdx.x; b <= E; b += kRouteThreads) sh_hist[b] = 0;
+  __syncthreads();
+  const int base = blockIdx.x * kRouteChunk;
+  for (int i = threadIdx.x; i < kRouteChunk; i += kRouteThreads) {
+    const int g = base + i;
+    if (g < M) atomicAdd(&sh_hist[bucket_of(labels, g, E)], 1);
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b <= E; b += kRouteThreads)
+    hist[(size_t)b * nchunks + blockIdx.x] = sh_hist[b];
+}
+
+__global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
+    int* __restrict__ hist, int n, int E, int nchunks, int M,
+    int* __restrict__ counts, int* __restrict__ offsets) {
+  extern __shared__ int sh_off[];  // E + 2
+  __shared__ int wave_sums[kScanThreads / kWave];
+  const int tid = threadIdx.x;
+  if (n == 0) {  // no labels at all
+    for (int e = tid; e <= E; e += kScanThreads) {
+      if (offsets) offsets[e] = 0;
+      if (e < E && counts) counts[e] = 0;
+    }
+    return;
+  }
+  const int per = (n + kScanThreads - 1) / kScanThreads;
+  const int lo = min(tid * per, n);
+  const int hi = min(lo + per, n);
+  int s = 0;
+  for (int i = lo; i < hi; ++i) s += hist[i];
+  const int incl = wave_inclusive_scan(s);
+  const int w = tid / kWave, l = lane_id();
+  if (l == kWave - 1) wave_sums[w] = incl;
+  __syncthreads();
+  if (w == 0) {
+    const int v = (l < kScanThreads / kWave) ? wave_sums[l] : 0;
+    const int vi = wave_inclusive_scan(v);
+    if (l < kScanThreads / kWave) wave_sums[l] = vi - v;
+  }
+  __syncthreads();
+  int run = wave_sums[w] + incl - s;
+  for (int i = lo; i < hi; ++i) {
+    const int c = hist[i];
+    hist[i] = run;
+    if (i % nchunks == 0) sh_off[i / nchunks] = run;
+    run += c;
+  }
+  if (tid == 0) sh_off[E + 1] = M;
+  __syncthreads();
+  for (int e = tid; e <= E; e += kScanThreads) {
+    if (offsets) offsets[e] = sh_off[e];
+    if (e < E && counts) counts[e] = sh_off[e + 1] - sh_off[e];
+  }
+}
+
+template <typename IdxT>
+__global__ __launch_bounds__(kRouteThreads) void route_rank_kernel(
+    const IdxT* __restrict__ labels, const float* __restrict__ scores, int M,
+    int E, int nbits, int nchunks, const int* __restrict__ base,
+    int* __restrict__ sorted_idx, int* __restrict__ inverse,
+    float* __restrict__ sorted_scores) {
+  extern __shared__ int sh_cnt[];  // [kRouteWaves][E + 1]
+  const int E1 = E + 1;
+  const int w = threadIdx.x / kWave, l = lane_id();
+  for (int i = threadIdx.x; i < kRouteWaves * E1; i += kRouteThreads) sh_cnt[i] = 0;
+  __syncthreads();
+
+  const int wbase = blockIdx.x * kRouteChunk + w * kRoutePerWave;
+  int bucket[kRoutePerWave / kWave];
+  uint64_t peers[kRoutePerWave / kWave];
+#pragma unroll
+  for (int s = 0; s < kRoutePerWave / kWave; ++s) {
+    const int g = wbase + s * kWave + l;
+    const bool valid = g < M;
+    const int b = valid ? bucket_of(labels, g, E) : 0;
+    uint64_t mask = ballot64(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool set = (b >> bit) & 1;
+      const uint64_t bb = ballot64(set);
+      mask &= set ? bb : ~bb;
+    }
+    bucket[s] = b;
+    peers[s] = mask;
+    // One leader per distinct bucket of this step: no two lanes of the wave
+    // touch the same counter, and other waves use their own row.
+    if (valid && l == (int)__builtin_ctzll(mask))
+      sh_cnt[w * E1 + b] += __builtin_popcountll(mask);
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+  // Running base of (wave w, bucket b) = chunk base + counts of earlier waves.
+  for (int b = threadIdx.x; b < E1; b += kRouteThreads) {
+    int run = base[(size_t)b * nchunks + blockIdx.x];
+#pragma unroll
+    for (int ww = 0; ww < kRouteWaves; ++ww) {
+      const int t = sh_cnt[ww * E1 + b];
+      sh_cnt[ww * E1 + b] = run;
+      run += t;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < kRoutePerWave / kWave; ++s) {
+    const int g = wbase + s * kWave + l;
+    const bool valid = g < M;
+    const int b = bucket[s];
+    const uint64_t mask = peers[s];
+    int pos = 0;
+    if (valid) pos = sh_cnt[w * E1 + b] + __builtin_popcountll(mask & lanemask_lt());
+    __builtin_amdgcn_wave_barrier();
+    if (valid && l == (int)__builtin_ctzll(mask))
+      sh_cnt[w * E1 + b] += __builtin_popcountll(mask);
+    __builtin_amdgcn_wave_barrier();
+    if (valid) {
+      pos = min(max(pos, 0), M - 1);
+      sorted_idx[pos] = g;
+      if (inverse) inverse[g] = pos;
+      if (sorted_scores) sorted_scores[pos] = scores[g];
+    }
+  }
+}
+
+size_t route_workspace_bytes(int64_t M, int E) {
+  const int64_t nchunks = (M + kRouteChunk - 1) / kRouteChunk;
+  return (size_t)((E + 1) * nchunks) * sizeof(int) + 256;
+}
+
+hipError_t launch_route(const void* labels, bool is64, int M, int E,
+                        const float* scores, int* counts, int* offsets,
+                        int* sorted_idx, int* inverse, float* sorted_scores,
+                        void* ws, hipStream_t stream) {
+  const int nchunks = (M + kRouteChunk - 1) / kRouteChunk;
+  int* hist = (int*)ws;
+  int nbits = 0;
+  while ((1 << nbits) <= E) ++nbits;  // bucket values 0..E
+  const size_t sh1 = (size_t)(E + 1) * sizeof(int);
+  const size_t sh2 = (size_t)(E + 2) * sizeof(int);
+  const size_t sh3 = (size_t)kRouteWaves * (E + 1) * sizeof(int);
+  if (M == 0) {
+    hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), sh2, stream,
+                       hist, 0, E, 1, 0, counts, offsets);
+    return hipGetLastError();
+  }
+  if (is64) {
+    hipLaunchKernelGGL(route_hist_kernel<int64_t>, dim3(nchunks), dim3(kRouteThreads), sh1,
+                       stream, (const int64_t*)labels, M, E, nchunks, hist);
+  } else {
+    hipLaunchKernelGGL(route_hist_kernel<int32_t>, dim3(nchunks), dim3(kRouteThreads), sh1,
+                       stream, (const int32_t*)labels, M, E, nchunks, hist);
+  }
+  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), sh2, stream, hist,
+                     (E + 1) * nchunks, E, nchunks, M, counts, offsets);
+  if (is64) {
+    hipLaunchKernelGGL(route_rank_kernel<int64_t>, dim3(nchunks), dim3(kRouteThreads), sh3,
+                       stream, (const int64_t*)labels, scores, M, E, nbits, nchunks, hist,
+                       sorted_idx, inverse, sorted_scores);
+  } else {
+    hipLaunchKernelGGL(route_rank_kernel<int32_t>, dim3(nchunks), dim3(kRouteThreads), sh3,
+                       stream, (const int32_t*)labels, scores, M, E, nbits, nchunks, hist,
+                       sorted_idx, inverse, sorted_scores);
+  }
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Row movement.  Rows are moved as 16-byte chunks (8 bf16); a thread handles
+// kUnroll chunks per iteration so several loads are in flight.
+// ---------------------------------------------------------------------------
+constexpr int kMoveThreads = 256;
+constexpr int kUnroll = 4;
+
+static int move_grid(int64_t total_chunks) {
+  int64_t g = (total_chunks + (int64_t)kMoveThreads * kUnroll - 1) / ((int64_t)kMoveThreads * kUnroll);
+  if (g < 1) g = 1;
+  if (g > 8192) g = 8192;
+  return (int)g;
+}
+
+// out[r] = in[clamp(src[r] / div)] * (scale ? scale[scale_by_src ? src[r] : r] : 1)
+__global__ __launch_bounds__(kMoveThreads) void gather_rows_kernel(
+    const uint4* __restrict__ in, const int* __restrict__ src,
+    const float* __restrict__ scale, int scale_by_src, int n_in, int n_src_max,
+    int rows, int cpr, int div, uint4* __restrict__ out) {
+  const int total = rows * cpr;
+  const int stride = gridDim.x * kMoveThreads;
+  for (int base = blockIdx.x * kMoveThreads + threadIdx.x; base < total; base += stride * kUnroll) {
+    uint4 v[kUnroll];
+    float sc[kUnroll];
+    int idx[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      idx[u] = base + u * stride;
+      sc[u] = 1.f;
+      if (idx[u] < total) {
+        const int r = idx[u] / cpr;
+        const int c = idx[u] - r * cpr;
+        int s = src ? src[r] : r;
+        s = min(max(s, 0), n_src_max - 1);
+        const int srow = min(s / div, n_in - 1);
+        v[u] = in[(size_t)srow * cpr + c];
+        if (scale) sc[u] = scale[scale_by_src ? s : r];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (idx[u] < total) {
+        if (scale) {
+          float f[8];
+          unpack8(v[u], f);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) f[i] *= sc[u];
+          v[u] = pack8(f);
+        }
+        out[idx[u]] = v[u];
+      }
+    }
+  }
+}
+
+hipError_t launch_gather_rows(const void* in, const int* src, const float* scale,
+                              bool scale_by_src, int n_in, int n_src_max, int rows,
+                              int hidden, int div, void* out, hipStream_t stream) {
+  const int cpr = hidden / 8;
+  const int64_t total = (int64_t)rows * cpr;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(move_grid(total)), dim3(kMoveThreads), 0, stream,
+                     (const uint4*)in, src, scale, scale_by_src ? 1 : 0, n_in, n_src_max, rows,
+                     cpr, div, (uint4*)out);
+  return hipGetLastError();
+}
+
+// inv[sorted[j]] = j.
+__global__ __launch_bounds__(kMoveThreads) void invert_perm_kernel(
+    const int* __restrict__ sorted, int M, int* __restrict__ inv) {
+  for (int j = blockIdx.x * kMoveThreads + threadIdx.x; j < M; j += gridDim.x * kMoveThreads) {
+    const int s = min(max(sorted[j], 0), M - 1);
+    inv[s] = j;
+  }
+}
+
+hipError_t launch_invert_perm(const int* sorted, int M, int* inv, hipStream_t stream) {
+  if (M == 0) return hipSuccess;
+  int g = (M + kMoveThreads - 1) / kMoveThreads;
+  if (g > 4096) g = 4096;
+  hipLaunchKernelGGL(invert_perm_kernel, dim3(g), dim3(kMoveThreads), 0, stream, sorted, M, inv);
+  return hipGetLastError();
+}
+
+// out[t] = sum_k w(t,k) * in[j(t,k)],  j = inverse ? inverse[t*topk+k] : t*topk+k.
+__global__ __launch_bounds__(kMoveThreads) void combine_kernel(
+    const uint4* __restrict__ in, const int* __restrict__ inverse,
+    const float* __restrict__ probs, int T, int topk, int M, int cpr,
+    uint4* __restrict__ out) {
+  const int total = T * cpr;
+  const int stride = gridDim.x * kMoveThreads;
+  for (int idx = blockIdx.x * kMoveThreads + threadIdx.x; idx < total; idx += stride) {
+    const int t = idx / cpr;
+    const int c = idx - t * cpr;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < topk; ++k) {
+      const int s = t * topk + k;
+      int j = inverse ? inverse[s] : s;
+      j = min(max(j, 0), M - 1);
+      const float w = probs ? probs[s] : 1.f;
+      float f[8];
+      unpack8(in[(size_t)j * cpr + c], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += w * f[i];
+    }
+    out[idx] = pack8(acc);
+  }
+}
+
+hipError_t launch_combine(const void* in, const int* inverse, const float* probs, int T,
+                          int topk, int hidden, void* out, hipStream_t stream) {
+  const int cpr = hidden / 8;
+  const int64_t total = (int64_t)T * cpr;
+  if (total == 0) return hipSuccess;
+  int64_t g = (total + kMoveThreads - 1) / kMoveThreads;
+  if (g > 8192) g = 8192;
+  hipLaunchKernelGGL(combine_kernel, dim3((int)g), dim3(kMoveThreads), 0, stream,
+                     (const uint4*)in, inverse, probs, T, topk, T * topk, cpr, (uint4*)out);
+  return hipGetLastError();
+}
+
+// out[o(j)] = <a[j], b[clamp(bidx[j] / bdiv)]>, o(j) = out_by_bidx ? bidx[j] : j.
+__global__ __launch_bounds__(kMoveThreads) void rowdot_kernel(
+    const uint4* __restrict__ a, const uint4* __restrict__ b, const int* __restrict__ bidx,
+    int bdiv, int out_by_bidx, int rows, int n_b, int n_out, int cpr,
+    float* __restrict__ out) {
+  const int wave = (blockIdx.x * kMoveThreads + threadIdx.x) / kWave;
+  const int nwaves = gridDim.x * kMoveThreads / kWave;
+  const int l = lane_id();
+  for (int j = wave; j < rows; j += nwaves) {
+    int s = bidx ? bidx[j] : j;
+    const int sb = min(max(s / bdiv, 0), n_b - 1);
+    float acc = 0.f;
+    for (int c = l; c < cpr; c += kWave) {
+      float fa[8], fb[8];
+      unpack8(a[(size_t)j * cpr + c], fa);
+      unpack8(b[(size_t)sb * cpr + c], fb);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc += fa[i] * fb[i];
+    }
+    acc = wave_reduce_sumf(acc);
+    if (l == 0) {
+      const int o = out_by_bidx ? min(max(s, 0), n_out - 1) : j;
+      out[o] = acc;
+    }
+  }
+}
+
+hipError_t launch_rowdot(const void* a, const void* b, const int* bidx, int bdiv,
+                         bool out_by_bidx, int rows, int n_b, int n_out, int hidden,
+                         float* out, hipStream_t stream) {
+  if (rows == 0) return hipSuccess;
+  int64_t g = ((int64_t)rows * kWave + kMoveThreads - 1) / kMoveThreads;
+  if (g > 8192) g = 8192;
+  hipLaunchKernelGGL(rowdot_kernel, dim3((int)g), dim3(kMoveThreads), 0, stream,
+                     (const uint4*)a, (const uint4*)b, bidx, bdiv, out_by_bidx ? 1 : 0, rows,
+                     n_b, n_out, hidden / 8, out);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Regroup labels: rows arrive as G consecutive groups (rank r, expert e),
+// g = r * E_loc + e; label = g % E_loc.  Each block scans the G counts in
+// LDS and binary-searches the group of each of its rows.
+// ---------------------------------------------------------------------------
+constexpr int kLabelMaxGroups = 8192;
+
+__global__ __launch_bounds__(kMoveThreads) void group_labels_kernel(
+    const int* __restrict__ counts, int G, int E_loc, int rows, int* __restrict__ labels) {
+  __shared__ int incl[kLabelMaxGroups];
+  __shared__ int wave_sums[kMoveThreads / kWave];
+  const int tid = threadIdx.x;
+  const int per = (G + kMoveThreads - 1) / kMoveThreads;
+  const int lo = min(tid * per, G), hi = min(lo + per, G);
+  int s = 0;
+  for (int i = lo; i < hi; ++i) s += max(counts[i], 0);
+  const int in = wave_inclusive_scan(s);
+  const int w = tid / kWave, l = lane_id();
+  if (l == kWave - 1) wave_sums[w] = in;
+  __syncthreads();
+  int base = 0;
+  for (int ww = 0; ww < w; ++ww) base += wave_sums[ww];
+  int run = base + in - s;
+  for (int i = lo; i < hi; ++i) {
+    run += max(counts[i], 0);
+    incl[i] = run;
+  }
+  __syncthreads();
+  const int total = incl[G - 1];
+  for (int j = blockIdx.x * kMoveThreads + tid; j < rows; j += gridDim.x * kMoveThreads) {
+    int lab = E_loc;
+    if (j < total) {
+      int a = 0, b = G - 1;  // first g with incl[g] > j
+      while (a < b) {
+        const int m = (a + b) >> 1;
+        if (incl[m] > j) b = m; else a = m + 1;
+      }
+      lab = a % E_loc;
+    }
+    labels[j] = lab;
+  }
+}
+
+hipError_t launch_group_labels(const int* counts_group, int G, int E_loc, int rows, int* labels,
+                               hipStream_t stream) {
+  if (rows == 0) return hipSuccess;
+  int g = (rows + kMoveThreads - 1) / kMoveThreads;
+  if (g > 1024) g = 1024;
+  hipLaunchKernelGGL(group_labels_kernel, dim3(g), dim3(kMoveThreads), 0, stream, counts_group, G,
+                     E_loc, rows, labels);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Router top-k: one wave per token.  Each lane holds ceil(E/64) scores in
+// registers; k rounds of a wave-wide (value desc, index asc) argmax.
+// ---------------------------------------------------------------------------
+constexpr int kTopkMaxPerLane = 16;  // E <= 1024
+
+template <int PER_LANE>
+__global__ __launch_bounds__(kMoveThreads) void router_topk_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int K,
+    int score_func, int renorm, float renorm_eps, float route_scale,
+    float* __restrict__ top_scores, int64_t* __restrict__ top_idx) {
+  const int wave = (blockIdx.x * kMoveThreads + threadIdx.x) / kWave;
+  const int nwaves = gridDim.x * kMoveThreads / kWave;
+  const int l = lane_id();
+  for (int t = wave; t < T; t += nwaves) {
+    const float* row = logits + (size_t)t * E;
+    float sc[PER_LANE], sel[PER_LANE];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PER_LANE; ++i) {
+      const int e = i * kWave + l;
+      sc[i] = (e < E) ? row[e] : -INFINITY;
+      mx = fmaxf(mx, sc[i]);
+    }
+    if (score_func == 0) {  // softmax in fp32
+#pragma unroll
+      for (int off = kWave / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+      float sum = 0.f;
+#pragma unroll
+      for (int i = 0; i < PER_LANE; ++i) {
+        const int e = i * kWave + l;
+        sc[i] = (e < E) ? expf(sc[i] - mx) : 0.f;
+        sum += sc[i];
+      }
+      sum = wave_reduce_sumf(sum);
+      const float inv = 1.f / sum;
+#pragma unroll
+      for (int i = 0; i < PER_LANE; ++i) sc[i] = sc[i] * inv;
+    } else {  // sigmoid
+#pragma unroll
+      for (int i = 0; i < PER_LANE; ++i) sc[i] = 1.f / (1.f + expf(-sc[i]));
+    }
+#pragma unroll
+    for (int i = 0; i < PER_LANE; ++i) {
+      const int e = i * kWave + l;
+      sel[i] = (e < E) ? (bias ? sc[i] + bias[e] : sc[i]) : -INFINITY;
+    }
+    float picked_sum = 0.f;
+    float my_val = 0.f;
+    int my_idx = 0;
+    for (int k = 0; k < K; ++k) {
+      // lane-local best (value desc, index asc)
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+#pragma unroll
+      for (int i = 0; i < PER_LANE; ++i) {
+        const int e = i * kWave + l;
+        if (e < E && (sel[i] > bv || (sel[i] == bv && e < bi))) {
+          bv = sel[i];
+          bi = e;
+        }
+      }
+#pragma unroll
+      for (int off = kWave / 2; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, kWave);
+        const int oi = __shfl_xor(bi, off, kWave);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      // bi is wave-uniform now; fetch its unbiased score from its owner lane.
+      const int owner = bi & (kWave - 1);
+      const int slot = bi / kWave;
+      float v = 0.f;
+#pragma unroll
+      for (int i = 0; i < PER_LANE; ++i)
+        if (i == slot) v = sc[i];
+      v = __shfl(v, owner, kWave);
+#pragma unroll
+      for (int i = 0; i < PER_LANE; ++i)
+        if (i == slot && l == owner) sel[i] = -INFINITY;
+      if (bi >= E) bi = 0;  // unreachable when K <= E; keeps the index in range
+      picked_sum += v;
+      if (l == k) {
+        my_val = v;
+        my_idx = bi;
+      }
+    }
+    if (l < K) {
+      float v = my_val;
+      if (renorm) v = v / (picked_sum + renorm_eps);
+      v *= route_scale;
+      top_scores[(size_t)t * K + l] = v;
+      top_idx[(size_t)t * K + l] = my_idx;
+    }
+  }
+}
+
+hipError_t launch_router_topk(const float* logits, const float* bias, int T, int E, int K,
+                              int score_func, int renorm, float renorm_eps, float route_scale,
+                              float* top_scores, int64_t* top_idx, hipStream_t stream) {
+  if (T == 0) return hipSuccess;
+  int64_t g = ((int64_t)T * kWave + kMoveThreads - 1) / kMoveThreads;
+  if (g > 8192) g = 8192;
+  const int per = (E + kWave - 1) / kWave;
+#define TTAMD_TOPK_CASE(P)                                                                     \
+  hipLaunchKernelGGL(router_topk_kernel<P>, dim3((int)g), dim3(kMoveThreads), 0, stream, logits, \
+                     bias, T, E, K, score_func, renorm, renorm_eps, route_scale, top_scores,    \
+                     top_idx)
+  if (per <= 1) {
+    TTAMD_TOPK_CASE(1);
+  } else if (per <= 2) {
+    TTAMD_TOPK_CASE(2);
+  } else if (per <= 4) {
+    TTAMD_TOPK_CASE(4);
+  } else if (per <= 8) {
+    TTAMD_TOPK_CASE(8);
+  } else {
+    TTAMD_TOPK_CASE(kTopkMaxPerLane);
+  }
+#undef TTAMD_TOPK_CASE
+  return hipGetLastError();
+}
+
+}  // namespace ttamd

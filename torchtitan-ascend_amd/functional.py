@@ -1,0 +1,194 @@
+"""Autograd functions of the MoE expert path (HIP kernels forward and backward).
+
+The split follows the reference's module boundaries so each piece can be used
+on its own:
+
+  dispatch  (upstream dispatch, entered from npu_gmm.py:106-108)
+      routed[j] = x[s_j // K] (* score[s_j] when score_before_experts)
+  experts   (_run_experts_grouped_mm, npu_gmm.py:21-40)
+      y = grouped_mm(swiglu(clamp(grouped_mm(routed, w13))), w2)
+  combine   (upstream combine, npu_gmm.py:110)
+      out[t] = sum_k (score[t,k] if score after experts else 1) * y[pos(t,k)]
+
+plus the reference's own NPUMoeTokenUnpermute (npu_permute.py:15-53).
+`moe_experts_forward` chains them; without autograd it takes the fused
+route: the score multiply and the un-permute run in the w2 GEMM epilogue.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+_BF16 = torch.bfloat16
+
+
+def _bf16(w: torch.Tensor) -> torch.Tensor:
+    return w if w.dtype == _BF16 else w.to(_BF16)
+
+
+class DispatchFn(torch.autograd.Function):
+    """routed = gather of token rows in stable expert order (+ score before experts)."""
+
+    @staticmethod
+    def forward(ctx, x, scores_flat, sorted_indices, inverse, sorted_scores, top_k, score_before):
+        ctx.top_k = top_k
+        ctx.score_before = score_before
+        routed = ops.gather_rows(x, sorted_indices, top_k, sorted_scores if score_before else None)
+        ctx.save_for_backward(x, scores_flat, sorted_indices, inverse)
+        return routed
+
+    @staticmethod
+    def backward(ctx, d_routed):
+        x, scores_flat, sorted_indices, inverse = ctx.saved_tensors
+        d_routed = d_routed.to(_BF16).contiguous()
+        dx = dscores = None
+        probs = scores_flat if ctx.score_before else None
+        if ctx.needs_input_grad[0]:
+            dx = ops.combine(d_routed, inverse, probs, ctx.top_k)
+        if ctx.score_before and ctx.needs_input_grad[1]:
+            # d score[s] = <d_routed[pos(s)], x[s // K]>
+            dscores = ops.rowdot_scatter(d_routed, x, sorted_indices, ctx.top_k)
+        return dx, dscores, None, None, None, None, None
+
+
+class ExpertsFn(torch.autograd.Function):
+    """y = (swiglu(clamp(x @ w13[e]^T))) @ w2[e]^T over ragged expert groups."""
+
+    @staticmethod
+    def forward(ctx, routed, w13, w2, offs, swiglu_limit):
+        w13b, w2b = _bf16(w13), _bf16(w2)
+        # autograd runs forward() with grad mode off; needs_input_grad says
+        # whether a backward can follow, i.e. whether h must be kept.
+        need = any(ctx.needs_input_grad[:3])
+        a, h = ops.grouped_mm_swiglu(routed, w13b, offs, swiglu_limit, save_h=need)
+        y = ops.grouped_mm_unpermute(a, w2b, offs)
+        ctx.swiglu_limit = swiglu_limit
+        ctx.w_dtypes = (w13.dtype, w2.dtype)
+        ctx.num_experts = w13.shape[0]
+        if need:
+            ctx.save_for_backward(routed, h, a, w13b, w2b, offs)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        routed, h, a, w13b, w2b, offs = ctx.saved_tensors
+        dy = dy.to(_BF16).contiguous()
+        E = ctx.num_experts
+        dh, _ = ops.grouped_mm_dgrad_swiglu(dy, w2b, h, offs, ctx.swiglu_limit)
+        d_routed = dw13 = dw2 = None
+        if ctx.needs_input_grad[2]:
+            dw2 = ops.grouped_mm_wgrad(dy, a, offs, E, torch.float32 if ctx.w_dtypes[1] != _BF16 else _BF16)
+            dw2 = dw2.to(ctx.w_dtypes[1])
+        if ctx.needs_input_grad[1]:
+            dw13 = ops.grouped_mm_wgrad(dh, routed, offs, E, torch.float32 if ctx.w_dtypes[0] != _BF16 else _BF16)
+            dw13 = dw13.to(ctx.w_dtypes[0])
+        if ctx.needs_input_grad[0]:
+            d_routed = ops.grouped_mm_dgrad(dh, w13b, offs)
+        return d_routed, dw13, dw2, None, None
+
+
+class CombineFn(torch.autograd.Function):
+    """out[t] = sum_k w(t,k) * y[pos(t,k)], w = score if score after experts else 1."""
+
+    @staticmethod
+    def forward(ctx, y, scores_flat, sorted_indices, inverse, top_k, score_after):
+        ctx.top_k = top_k
+        ctx.score_after = score_after
+        probs = scores_flat if score_after else None
+        out = ops.combine(y, inverse, probs, top_k)
+        ctx.save_for_backward(y, scores_flat, sorted_indices)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        y, scores_flat, sorted_indices = ctx.saved_tensors
+        dout = dout.to(_BF16).contiguous()
+        need_ds = ctx.score_after and ctx.needs_input_grad[1]
+        dy, dscores = ops.token_unpermute_grad(
+            dout, sorted_indices, scores_flat if ctx.score_after else None, y if need_ds else None,
+            ctx.top_k, need_probs_grad=need_ds,
+        )
+        return dy, dscores, None, None, None, None
+
+
+class HIPMoeTokenUnpermute(torch.autograd.Function):
+    """Functional unpermute with backward; same contract as the reference's
+    NPUMoeTokenUnpermute (torchtitanturbo/models/common/npu_permute.py:15-53):
+    probs=None, top_k=1, empty input passes through."""
+
+    @staticmethod
+    def forward(ctx, permuted_tokens, sorted_indices, restore_shape):
+        if not permuted_tokens.numel():
+            return permuted_tokens
+        out = ops.token_unpermute(permuted_tokens, sorted_indices, None, 1)
+        ctx.restore_shape = restore_shape
+        ctx.save_for_backward(sorted_indices)
+        return out.view(restore_shape)
+
+    @staticmethod
+    def backward(ctx, unpermuted_tokens_grad):
+        if not unpermuted_tokens_grad.numel():
+            return unpermuted_tokens_grad, None, None
+        if ctx.needs_input_grad[0]:
+            (sorted_indices,) = ctx.saved_tensors
+            g = unpermuted_tokens_grad.reshape(-1, unpermuted_tokens_grad.shape[-1]).to(_BF16).contiguous()
+            act_grad, _ = ops.token_unpermute_grad(g, sorted_indices, None, None, 1)
+            return act_grad, None, None
+        return None, None, None
+
+
+def run_experts_grouped_mm(
+    w13: torch.Tensor,
+    w2: torch.Tensor,
+    x: torch.Tensor,
+    num_tokens_per_expert: torch.Tensor,
+    swiglu_limit: float | None = None,
+) -> torch.Tensor:
+    """Same signature and result as the reference's _run_experts_grouped_mm
+    (torchtitanturbo/models/common/npu_gmm.py:21-40), on the HIP kernels."""
+    offs = torch.cumsum(num_tokens_per_expert, dim=0, dtype=torch.int32)
+    y = ExpertsFn.apply(x.to(_BF16).contiguous(), w13, w2, offs, swiglu_limit)
+    return y.type_as(x)
+
+
+def moe_experts_forward(
+    x: torch.Tensor,
+    top_scores: torch.Tensor,
+    selected_experts_indices: torch.Tensor,
+    w13: torch.Tensor,
+    w2: torch.Tensor,
+    num_experts: int,
+    score_before_experts: bool,
+    swiglu_limit: float | None = None,
+) -> torch.Tensor:
+    """dispatch -> experts -> combine for one GPU; x [T, D], scores/indices [T, K] -> [T, D].
+
+    With autograd off (or nothing requiring grad) the score multiply and the
+    un-permute are fused into the w2 GEMM epilogue.
+    """
+    T, D = x.shape
+    K = top_scores.shape[-1]
+    scores_flat = top_scores.reshape(-1).float()
+    r = ops.route(selected_experts_indices, num_experts, scores_flat)
+    offs = r.offs
+    xb = x.to(_BF16).contiguous()
+    training = torch.is_grad_enabled() and any(
+        t.requires_grad for t in (x, top_scores, w13, w2)
+    )
+    if not training:
+        routed = ops.gather_rows(xb, r.sorted_indices, K, r.sorted_scores if score_before_experts else None)
+        a, _ = ops.grouped_mm_swiglu(routed, _bf16(w13), offs, swiglu_limit)
+        scale = None if score_before_experts else r.sorted_scores
+        if K == 1:
+            out = ops.grouped_mm_unpermute(a, _bf16(w2), offs, scale, r.sorted_indices, T)
+        else:
+            ybuf = ops.grouped_mm_unpermute(a, _bf16(w2), offs, scale, r.sorted_indices, T * K)
+            out = ops.sum_topk(ybuf, K)
+        return out.to(x.dtype)
+    routed = DispatchFn.apply(
+        xb, scores_flat, r.sorted_indices, r.inverse, r.sorted_scores, K, score_before_experts
+    )
+    y = ExpertsFn.apply(routed, w13, w2, offs, swiglu_limit)
+    out = CombineFn.apply(y, scores_flat, r.sorted_indices, r.inverse, K, not score_before_experts)
+    return out.to(x.dtype)

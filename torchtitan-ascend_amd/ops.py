@@ -1,0 +1,472 @@
+"""Torch-facing functional ops of the MoE expert path.
+
+Every op allocates its outputs with torch's caching allocator, then calls the
+C ABI of libttamd_moe.so on torch's current HIP stream.  There is no CPU or
+eager-torch fallback: tensors must live on a HIP device and the library must
+be built, otherwise the op raises.
+
+Conventions (shared with include/ttamd_moe.h):
+  * bf16 activations/weights, fp32 routing scores, int32 index maps;
+  * flat slot s = t * top_k + k (the order of selected_experts_indices.view(-1));
+  * `offs` = inclusive cumsum of per-expert row counts, int32 [E]
+    (torchtitanturbo/models/common/npu_gmm.py:29).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+_BF16 = torch.bfloat16
+
+
+def _p(t: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _gpu(name: str, t: torch.Tensor) -> torch.device:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"{name} is on {t.device}; the MoE expert path runs only on a HIP device (no CPU fallback)"
+        )
+    return t.device
+
+
+def _same_device(dev: torch.device, **tensors) -> None:
+    for name, t in tensors.items():
+        if t is not None and t.device != dev:
+            raise RuntimeError(f"{name} is on {t.device}, expected {dev}")
+
+
+def _want(name: str, t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    return t.contiguous()
+
+
+def _ws(nbytes: int, dev: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=dev)
+
+
+def _limit(swiglu_limit: float | None) -> float:
+    if swiglu_limit is None:
+        return math.nan
+    if swiglu_limit < 0:
+        raise ValueError(f"swiglu_limit must be >= 0 or None, got {swiglu_limit}")
+    return float(swiglu_limit)
+
+
+# ---------------------------------------------------------------------------
+# Routing
+# ---------------------------------------------------------------------------
+@dataclass
+class RouteResult:
+    """Output of `route`: histogram, group offsets and the stable order."""
+
+    counts: torch.Tensor  # int32 [E]
+    offsets: torch.Tensor  # int32 [E+1], exclusive (offsets[0] = 0)
+    sorted_indices: torch.Tensor  # int32 [M]: j-th flat slot in stable expert order
+    inverse: torch.Tensor  # int32 [M]: position of flat slot s
+    sorted_scores: torch.Tensor | None  # fp32 [M] or None
+
+    @property
+    def offs(self) -> torch.Tensor:
+        """Inclusive offsets int32 [E] in torch._grouped_mm's convention."""
+        return self.offsets[1:]
+
+
+def router_topk(
+    logits: torch.Tensor,
+    top_k: int,
+    score_func: str = "softmax",
+    route_norm: bool = False,
+    route_scale: float = 1.0,
+    expert_bias: torch.Tensor | None = None,
+    norm_eps: float = 1e-20,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Top-k selection of the router (upstream TokenChoiceTopKRouter; in-reference
+    closed form torchtitanturbo/models/qwen3_5/model.py:757-765).
+
+    Returns (top_scores fp32 [T, K], selected_experts_indices int64 [T, K]),
+    sorted by descending score, ties broken towards the lower expert id.
+    """
+    dev = _gpu("logits", logits)
+    if logits.dim() != 2:
+        raise ValueError("logits must be [T, E]")
+    logits = logits.float().contiguous()
+    T, E = logits.shape
+    funcs = {"softmax": 0, "sigmoid": 1}
+    if score_func not in funcs:
+        raise ValueError(f"score_func must be one of {sorted(funcs)}")
+    if expert_bias is not None:
+        _same_device(dev, expert_bias=expert_bias)
+        expert_bias = expert_bias.float().contiguous()
+        if expert_bias.shape != (E,):
+            raise ValueError("expert_bias must be [E]")
+    scores = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+    idx = torch.empty(T, top_k, dtype=torch.int64, device=dev)
+    _lib.call(
+        "ttamd_router_topk", _p(logits), _p(expert_bias), T, E, top_k, funcs[score_func],
+        int(bool(route_norm)), float(norm_eps), float(route_scale), _p(scores), _p(idx), _stream(dev),
+    )
+    return scores, idx
+
+
+def route(
+    selected_experts_indices: torch.Tensor,
+    num_experts: int,
+    scores: torch.Tensor | None = None,
+) -> RouteResult:
+    """Histogram + stable counting sort of the flat expert labels.
+
+    Bit-exact equivalent of upstream dispatch's
+    `histc(idx.view(-1), bins=E)` and `argsort(idx.view(-1), stable=True)`
+    (reached from torchtitanturbo/models/common/npu_gmm.py:106-108).
+    """
+    dev = _gpu("selected_experts_indices", selected_experts_indices)
+    labels = selected_experts_indices.reshape(-1)
+    if labels.dtype not in (torch.int64, torch.int32):
+        raise TypeError("expert indices must be int64 or int32")
+    labels = labels.contiguous()
+    M = labels.numel()
+    counts = torch.empty(num_experts, dtype=torch.int32, device=dev)
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    sorted_idx = torch.empty(M, dtype=torch.int32, device=dev)
+    inverse = torch.empty(M, dtype=torch.int32, device=dev)
+    sorted_scores = None
+    sc = None
+    if scores is not None:
+        _same_device(dev, scores=scores)
+        sc = scores.reshape(-1).float().contiguous()
+        if sc.numel() != M:
+            raise ValueError("scores must have one entry per expert choice")
+        sorted_scores = torch.empty(M, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    wsb = lib.ttamd_route_workspace_bytes(M, num_experts)
+    ws = _ws(wsb, dev)
+    _lib.call(
+        "ttamd_moe_route", _p(labels), int(labels.dtype == torch.int64), M, num_experts, _p(sc),
+        _p(counts), _p(offsets), _p(sorted_idx), _p(inverse), _p(sorted_scores), _p(ws), ws.numel(),
+        _stream(dev),
+    )
+    return RouteResult(counts, offsets, sorted_idx, inverse, sorted_scores)
+
+
+def gather_rows(
+    x: torch.Tensor, src_index: torch.Tensor, top_k: int = 1, row_scale: torch.Tensor | None = None
+) -> torch.Tensor:
+    """out[j] = x[src_index[j] // top_k] (* row_scale[j] in fp32, rounded once)."""
+    dev = _gpu("x", x)
+    x = _want("x", x, _BF16)
+    src_index = _want("src_index", src_index, torch.int32)
+    _same_device(dev, src_index=src_index, row_scale=row_scale)
+    rows = src_index.numel()
+    D = x.shape[-1]
+    out = torch.empty(rows, D, dtype=_BF16, device=dev)
+    if row_scale is not None:
+        row_scale = _want("row_scale", row_scale, torch.float32)
+    _lib.call(
+        "ttamd_moe_gather_rows", _p(x), _p(src_index), _p(row_scale), x.numel() // D, rows, D, top_k,
+        _p(out), _stream(dev),
+    )
+    return out
+
+
+def token_permute(
+    tokens: torch.Tensor, indices: torch.Tensor, num_experts: int, return_counts: bool = False
+):
+    """Drop-in for torch_npu.npu_moe_token_permute(tokens, indices)
+    (torchtitanturbo/models/common/npu_permute.py:74-76).
+
+    indices [T] or [T, K] expert labels; returns (permuted [T*K, D],
+    sorted_indices int32 [T*K]) with sorted_indices the stable argsort of the
+    flat labels.  `num_experts` bounds the label range.
+    """
+    dev = _gpu("tokens", tokens)
+    tokens = _want("tokens", tokens, _BF16)
+    _same_device(dev, indices=indices)
+    T, D = tokens.shape
+    topk = 1 if indices.dim() == 1 else indices.shape[-1]
+    labels = indices.reshape(-1).contiguous()
+    if labels.dtype not in (torch.int64, torch.int32):
+        raise TypeError("indices must be int64 or int32")
+    if labels.numel() != T * topk:
+        raise ValueError("indices must have T * top_k entries")
+    M = T * topk
+    permuted = torch.empty(M, D, dtype=_BF16, device=dev)
+    sorted_idx = torch.empty(M, dtype=torch.int32, device=dev)
+    counts = torch.empty(num_experts, dtype=torch.int32, device=dev)
+    lib = _lib.load()
+    ws = _ws(lib.ttamd_route_workspace_bytes(M, num_experts), dev)
+    _lib.call(
+        "ttamd_moe_token_permute", _p(tokens), _p(labels), int(labels.dtype == torch.int64), T, D, topk,
+        num_experts, _p(permuted), _p(sorted_idx), _p(counts), _p(ws), ws.numel(), _stream(dev),
+    )
+    if return_counts:
+        return permuted, sorted_idx, counts
+    return permuted, sorted_idx
+
+
+def token_unpermute(
+    permuted: torch.Tensor,
+    sorted_indices: torch.Tensor,
+    probs: torch.Tensor | None = None,
+    top_k: int = 1,
+) -> torch.Tensor:
+    """Drop-in for torch_npu._npu_moe_token_unpermute_with_routing_map
+    (npu_permute.py:23-30): out[t] = sum_k probs[t,k] * permuted[j(t,k)]."""
+    dev = _gpu("permuted", permuted)
+    permuted = _want("permuted", permuted, _BF16)
+    sorted_indices = _want("sorted_indices", sorted_indices, torch.int32)
+    _same_device(dev, sorted_indices=sorted_indices, probs=probs)
+    M, D = permuted.shape
+    if M % top_k:
+        raise ValueError("permuted rows must be a multiple of top_k")
+    T = M // top_k
+    if probs is not None:
+        probs = probs.reshape(-1).float().contiguous()
+    out = torch.empty(T, D, dtype=_BF16, device=dev)
+    lib = _lib.load()
+    ws = _ws(lib.ttamd_unpermute_workspace_bytes(T, top_k), dev)
+    _lib.call(
+        "ttamd_moe_token_unpermute", _p(permuted), _p(sorted_indices), _p(probs), T, D, top_k, _p(out),
+        _p(ws), ws.numel(), _stream(dev),
+    )
+    return out
+
+
+def token_unpermute_grad(
+    grad_out: torch.Tensor,
+    sorted_indices: torch.Tensor,
+    probs: torch.Tensor | None = None,
+    permuted: torch.Tensor | None = None,
+    top_k: int = 1,
+    need_probs_grad: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Drop-in for torch_npu.npu_moe_token_unpermute_with_routing_map_grad
+    (npu_permute.py:41-50).  Returns (grad_permuted, grad_probs or None)."""
+    dev = _gpu("grad_out", grad_out)
+    grad_out = _want("grad_out", grad_out, _BF16)
+    sorted_indices = _want("sorted_indices", sorted_indices, torch.int32)
+    T, D = grad_out.shape
+    M = T * top_k
+    if probs is not None:
+        probs = probs.reshape(-1).float().contiguous()
+    gp = None
+    if need_probs_grad:
+        if probs is None or permuted is None:
+            raise ValueError("probs gradient needs probs and permuted")
+        permuted = _want("permuted", permuted, _BF16)
+        gp = torch.empty(M, dtype=torch.float32, device=dev)
+    g = torch.empty(M, D, dtype=_BF16, device=dev)
+    _lib.call(
+        "ttamd_moe_token_unpermute_grad", _p(grad_out), _p(sorted_indices), _p(probs),
+        _p(permuted if need_probs_grad else None), T, D, top_k, _p(g), _p(gp), _stream(dev),
+    )
+    return g, gp
+
+
+def combine(
+    permuted: torch.Tensor, inverse: torch.Tensor, probs: torch.Tensor | None, top_k: int
+) -> torch.Tensor:
+    """out[t] = sum_k probs[t,k] * permuted[inverse[t*K+k]] (fp32 accumulate)."""
+    dev = _gpu("permuted", permuted)
+    permuted = _want("permuted", permuted, _BF16)
+    inverse = _want("inverse", inverse, torch.int32)
+    M, D = permuted.shape
+    T = M // top_k
+    if probs is not None:
+        probs = probs.reshape(-1).float().contiguous()
+    out = torch.empty(T, D, dtype=_BF16, device=dev)
+    _lib.call("ttamd_moe_combine", _p(permuted), _p(inverse), _p(probs), T, D, top_k, _p(out), _stream(dev))
+    return out
+
+
+def rowdot_scatter(a: torch.Tensor, b: torch.Tensor, index: torch.Tensor, div: int) -> torch.Tensor:
+    """out[index[j]] = <a[j], b[index[j] // div]> in fp32 (a and out have the same rows)."""
+    dev = _gpu("a", a)
+    a = _want("a", a, _BF16)
+    b = _want("b", b, _BF16)
+    index = _want("index", index, torch.int32)
+    out = torch.empty(a.shape[0], dtype=torch.float32, device=dev)
+    _lib.call(
+        "ttamd_moe_rowdot", _p(a), _p(b), _p(index), div, 1, a.shape[0], b.shape[0], a.shape[1], _p(out),
+        _stream(dev),
+    )
+    return out
+
+
+def sum_topk(y: torch.Tensor, top_k: int) -> torch.Tensor:
+    dev = _gpu("y", y)
+    y = _want("y", y, _BF16)
+    M, D = y.shape
+    out = torch.empty(M // top_k, D, dtype=_BF16, device=dev)
+    _lib.call("ttamd_moe_sum_topk", _p(y), M // top_k, D, top_k, _p(out), _stream(dev))
+    return out
+
+
+def group_labels(counts_group: torch.Tensor, num_local_experts: int, num_rows: int) -> torch.Tensor:
+    """Labels of rows grouped (rank, local expert): row in group g gets g % E_loc
+    (torchtitanturbo/models/common/npu_permute.py:68-72), computed without a host sync."""
+    dev = _gpu("counts_group", counts_group)
+    cg = counts_group.reshape(-1).to(torch.int32).contiguous()
+    out = torch.empty(num_rows, dtype=torch.int32, device=dev)
+    _lib.call("ttamd_moe_group_labels", _p(cg), cg.numel(), num_local_experts, num_rows, _p(out), _stream(dev))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Grouped GEMMs
+# ---------------------------------------------------------------------------
+def _gemm_ws(M: int, E: int, dev: torch.device) -> torch.Tensor:
+    return _ws(_lib.load().ttamd_gemm_workspace_bytes(M, E), dev)
+
+
+def _offs(offs: torch.Tensor, dev: torch.device) -> torch.Tensor:
+    _same_device(dev, offs=offs)
+    if offs.dtype != torch.int32:
+        offs = offs.to(torch.int32)
+    return offs.contiguous()
+
+
+def grouped_mm(x: torch.Tensor, w: torch.Tensor, offs: torch.Tensor) -> torch.Tensor:
+    """out[m] = x[m] @ w[e(m)]^T, w [E, N, K]; torch._grouped_mm(x, w.transpose(-2, -1), offs)
+    as called at torchtitanturbo/models/common/npu_gmm.py:17-18."""
+    dev = _gpu("x", x)
+    x = _want("x", x, _BF16)
+    w = _want("w", w, _BF16)
+    offs = _offs(offs, dev)
+    M, K = x.shape
+    E, N, K2 = w.shape
+    if K2 != K:
+        raise ValueError(f"x has K={K}, w has K={K2}")
+    out = torch.empty(M, N, dtype=_BF16, device=dev)
+    ws = _gemm_ws(M, E, dev)
+    _lib.call("ttamd_grouped_mm", _p(x), _p(w), _p(offs), M, E, N, K, _p(out), _p(ws), ws.numel(), _stream(dev))
+    return out
+
+
+def grouped_mm_swiglu(
+    x: torch.Tensor, w13: torch.Tensor, offs: torch.Tensor, swiglu_limit: float | None = None, save_h: bool = False
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """a = swiglu(clamp(x @ w13[e]^T)) (npu_gmm.py:29-37); returns (a [M,H], h [M,2H] or None)."""
+    dev = _gpu("x", x)
+    x = _want("x", x, _BF16)
+    w13 = _want("w13", w13, _BF16)
+    offs = _offs(offs, dev)
+    M, D = x.shape
+    E, H2, D2 = w13.shape
+    if D2 != D or H2 % 2:
+        raise ValueError(f"w13 must be [E, 2H, {D}], got {tuple(w13.shape)}")
+    H = H2 // 2
+    a = torch.empty(M, H, dtype=_BF16, device=dev)
+    h = torch.empty(M, 2 * H, dtype=_BF16, device=dev) if save_h else None
+    ws = _gemm_ws(M, E, dev)
+    _lib.call(
+        "ttamd_grouped_mm_swiglu", _p(x), _p(w13), _p(offs), M, E, H, D, _limit(swiglu_limit), _p(a), _p(h),
+        _p(ws), ws.numel(), _stream(dev),
+    )
+    return a, h
+
+
+def grouped_mm_unpermute(
+    a: torch.Tensor,
+    w2: torch.Tensor,
+    offs: torch.Tensor,
+    row_scale: torch.Tensor | None = None,
+    dest: torch.Tensor | None = None,
+    num_dest_rows: int | None = None,
+) -> torch.Tensor:
+    """out[dest[j]] = row_scale[j] * (a[j] @ w2[e(j)]^T), w2 [E, D, H] (npu_gmm.py:38 + combine)."""
+    dev = _gpu("a", a)
+    a = _want("a", a, _BF16)
+    w2 = _want("w2", w2, _BF16)
+    offs = _offs(offs, dev)
+    M, H = a.shape
+    E, D, H2 = w2.shape
+    if H2 != H:
+        raise ValueError(f"w2 must be [E, D, {H}], got {tuple(w2.shape)}")
+    if row_scale is not None:
+        row_scale = _want("row_scale", row_scale, torch.float32)
+    if dest is not None:
+        dest = _want("dest", dest, torch.int32)
+    nd = M if num_dest_rows is None else int(num_dest_rows)
+    out = torch.empty(nd, D, dtype=_BF16, device=dev)
+    ws = _gemm_ws(M, E, dev)
+    _lib.call(
+        "ttamd_grouped_mm_unpermute", _p(a), _p(w2), _p(offs), M, E, D, H, _p(row_scale), _p(dest), nd, _p(out),
+        _p(ws), ws.numel(), _stream(dev),
+    )
+    return out
+
+
+def grouped_mm_dgrad(dy: torch.Tensor, w: torch.Tensor, offs: torch.Tensor) -> torch.Tensor:
+    """dx[m] = dy[m] @ w[e(m)], w [E, N, K] (backward of grouped_mm w.r.t. x)."""
+    dev = _gpu("dy", dy)
+    dy = _want("dy", dy, _BF16)
+    w = _want("w", w, _BF16)
+    offs = _offs(offs, dev)
+    M, N = dy.shape
+    E, N2, K = w.shape
+    if N2 != N:
+        raise ValueError("dy and w disagree on N")
+    dx = torch.empty(M, K, dtype=_BF16, device=dev)
+    ws = _gemm_ws(M, E, dev)
+    _lib.call("ttamd_grouped_mm_dgrad", _p(dy), _p(w), _p(offs), M, E, N, K, _p(dx), _p(ws), ws.numel(), _stream(dev))
+    return dx
+
+
+def grouped_mm_dgrad_swiglu(
+    dy: torch.Tensor, w2: torch.Tensor, h: torch.Tensor, offs: torch.Tensor,
+    swiglu_limit: float | None = None, want_a: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """dh = swiglu_backward(dy @ w2[e], h); returns (dh [M, 2H], a [M, H] or None)."""
+    dev = _gpu("dy", dy)
+    dy = _want("dy", dy, _BF16)
+    w2 = _want("w2", w2, _BF16)
+    h = _want("h", h, _BF16)
+    offs = _offs(offs, dev)
+    M, D = dy.shape
+    E, D2, H = w2.shape
+    if D2 != D or h.shape != (M, 2 * H):
+        raise ValueError("dy, w2 and h shapes disagree")
+    dh = torch.empty(M, 2 * H, dtype=_BF16, device=dev)
+    a = torch.empty(M, H, dtype=_BF16, device=dev) if want_a else None
+    ws = _gemm_ws(M, E, dev)
+    _lib.call(
+        "ttamd_grouped_mm_dgrad_swiglu", _p(dy), _p(w2), _p(h), _p(offs), M, E, D, H, _limit(swiglu_limit),
+        _p(dh), _p(a), _p(ws), ws.numel(), _stream(dev),
+    )
+    return dh, a
+
+
+def grouped_mm_wgrad(
+    dy: torch.Tensor, x: torch.Tensor, offs: torch.Tensor, num_experts: int, out_dtype: torch.dtype = torch.float32
+) -> torch.Tensor:
+    """dw[e] = dy_e^T @ x_e over each expert's rows; dw [E, N, K] in out_dtype (fp32 or bf16)."""
+    dev = _gpu("dy", dy)
+    dy = _want("dy", dy, _BF16)
+    x = _want("x", x, _BF16)
+    offs = _offs(offs, dev)
+    M, N = dy.shape
+    M2, K = x.shape
+    if M2 != M:
+        raise ValueError("dy and x must have the same rows")
+    if out_dtype not in (torch.float32, _BF16):
+        raise TypeError("wgrad output must be float32 or bfloat16")
+    dw = torch.empty(num_experts, N, K, dtype=out_dtype, device=dev)
+    _lib.call(
+        "ttamd_grouped_mm_wgrad", _p(dy), _p(x), _p(offs), M, num_experts, N, K, _p(dw),
+        int(out_dtype == torch.float32), None, 0, _stream(dev),
+    )
+    return dw
