@@ -271,11 +271,17 @@ def _unpermute_f32(y, sidx, probs, K):
 
 
 def moe_backward(x, top_scores, idx, w13, w2, num_experts, score_before_experts, dout,
-                 swiglu_limit: float | None = None):
-    """Gradients of moe_forward (fp32 throughout, no intermediate rounding):
-    returns dict(dx [T,D], dscores [T,K], dw13 [E,2H,D], dw2 [E,D,H]).
-    The chain is the autograd of npu_gmm.py:21-40 plus the UPSTREAM
-    dispatch/combine score multiplies."""
+                 swiglu_limit: float | None = None, round_intermediates: bool = False):
+    """Gradients of moe_forward: returns dict(dx [T,D], dscores [T,K],
+    dw13 [E,2H,D], dw2 [E,D,H]).  The chain is the autograd of
+    npu_gmm.py:21-40 plus the UPSTREAM dispatch/combine score multiplies.
+
+    Gradients are accumulated in fp32.  With round_intermediates the forward
+    values the reference materialises in bf16 are rounded where it rounds
+    them: the dispatched rows (score before experts), the grouped_mm output
+    h (npu_gmm.py:31; the clamp masks of :32-36 are taken from this bf16 h),
+    the SwiGLU output a (:37) and the w2 output y (:38)."""
+    rnd = bf16_round if round_intermediates else (lambda v: v)
     x = np.asarray(x, np.float32)
     T, D = x.shape
     K = top_scores.shape[-1]
@@ -287,10 +293,10 @@ def moe_backward(x, top_scores, idx, w13, w2, num_experts, score_before_experts,
     offs = np.cumsum(counts)
     tok = sidx // K
     xr = x[tok]
-    routed = xr * s_flat[sidx][:, None] if score_before_experts else xr
-    h = grouped_mm(routed, w13, offs)
-    a = swiglu(h, swiglu_limit)
-    y = grouped_mm(a, w2, offs)
+    routed = rnd(xr * s_flat[sidx][:, None]) if score_before_experts else xr
+    h = rnd(grouped_mm(routed, w13, offs))
+    a = rnd(swiglu(h, swiglu_limit))
+    y = rnd(grouped_mm(a, w2, offs))
     dout = np.asarray(dout, np.float32)
     g_tok = dout[tok]  # dOut gathered per routed row
     dscores = np.zeros(T * K, np.float32)
