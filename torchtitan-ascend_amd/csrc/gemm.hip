@@ -26,6 +26,7 @@
 //   :32-36            optional clamp with swiglu_limit
 //   :37               npu_swiglu: silu(gate) * up, gate = first H columns
 #include "common.h"
+#include "gemm_common.h"
 #include "kernels.h"
 
 namespace ttamd {
@@ -47,7 +48,8 @@ __device__ __forceinline__ int lds_off(int r, int c) { return r * BK + swz(r, c)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void tile_map_kernel(const int* __restrict__ offs, int E,
                                                         int M, int max_tiles,
-                                                        int4* __restrict__ table) {
+                                                        int4* __restrict__ table,
+                                                        int* __restrict__ count) {
   __shared__ int wave_sums[16];
   const int tid = threadIdx.x;
   int r0 = 0, r1 = 0, nt = 0;
@@ -75,6 +77,14 @@ __global__ __launch_bounds__(1024) void tile_map_kernel(const int* __restrict__ 
     if (i < max_tiles) table[i] = make_int4(tid, r0 + t * BQ, min(r0 + (t + 1) * BQ, r1), 0);
   }
   for (int i = total + tid; i < max_tiles; i += 1024) table[i] = make_int4(-1, 0, 0, 0);
+  if (tid == 0) *count = min(total, max_tiles);
+}
+
+hipError_t launch_tile_map(const int* offs, int E, int M, void* ws, hipStream_t stream) {
+  TileTable tt = tile_table_in(ws);
+  hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, stream, offs, E, M,
+                     max_row_tiles(M, E), tt.table, tt.count);
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -157,13 +167,6 @@ __device__ __forceinline__ void mfma_step(const bf16_t* ldsP, const bf16_t* ldsQ
 // ---------------------------------------------------------------------------
 // Rows kernel (forward and dgrad).
 // ---------------------------------------------------------------------------
-enum Epi {
-  EPI_STORE = 0,       // out[q][p] = acc
-  EPI_SWIGLU = 1,      // P tile = 64 gate rows + 64 up rows; out = silu(g) * u
-  EPI_SCATTER = 2,     // out[dest[q]][p] = scale[q] * acc
-  EPI_SWIGLU_BWD = 3,  // dh from dA = acc and saved h
-};
-
 struct RowsArgs {
   const bf16_t* q;  // activations [M][Kred], k contiguous
   int64_t ldq;
@@ -189,10 +192,6 @@ struct RowsArgs {
   const int* dest;
   int n_dest;
 };
-
-__device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
-
-__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
 template <int EPI, bool P_TRANS>
 __global__ __launch_bounds__(kGemmThreads) void gg_rows_kernel(const RowsArgs args) {
@@ -511,10 +510,10 @@ __global__ __launch_bounds__(kGemmThreads) void gg_wgrad_kernel(const WgradArgs 
 // ---------------------------------------------------------------------------
 // Host-side launchers.
 // ---------------------------------------------------------------------------
-int gemm_max_qtiles(int M, int E) { return M / BQ + E + 1; }
+int gemm_max_qtiles(int M, int E) { return max_row_tiles(M, E); }
 
 size_t gemm_workspace_bytes(int64_t M, int E) {
-  return (size_t)gemm_max_qtiles((int)M, E) * sizeof(int4) + 256;
+  return (size_t)(max_row_tiles((int)M, E) + 1) * sizeof(int4) + 256;
 }
 
 static int round_up8(int x) { return (x + 7) & ~7; }
@@ -522,58 +521,54 @@ static int round_up8(int x) { return (x + 7) & ~7; }
 static hipError_t launch_rows(int epi, bool ptrans, RowsArgs a, const int* offs, int E, int M,
                               void* ws, hipStream_t stream) {
   const int max_q = gemm_max_qtiles(M, E);
-  int4* table = (int4*)ws;
-  hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, stream, offs, E, M, max_q, table);
-  a.table = table;
+  hipError_t err = launch_tile_map(offs, E, M, ws, stream);
+  if (err != hipSuccess) return err;
+  a.table = tile_table_in(ws).table;
   a.max_qtiles = max_q;
   const int grid = round_up8(max_q * a.np_tiles);
   a.grid_per_xcd = grid / 8;
-  if (epi == EPI_STORE && !ptrans)
-    hipLaunchKernelGGL((gg_rows_kernel<EPI_STORE, false>), dim3(grid), dim3(kGemmThreads), 0, stream, a);
-  else if (epi == EPI_STORE && ptrans)
+  // Only the dgrad orientation (weight reduction index strided) runs here.
+  if (!ptrans) return hipErrorInvalidValue;
+  if (epi == EPI_STORE)
     hipLaunchKernelGGL((gg_rows_kernel<EPI_STORE, true>), dim3(grid), dim3(kGemmThreads), 0, stream, a);
-  else if (epi == EPI_SWIGLU)
-    hipLaunchKernelGGL((gg_rows_kernel<EPI_SWIGLU, false>), dim3(grid), dim3(kGemmThreads), 0, stream, a);
-  else if (epi == EPI_SCATTER)
-    hipLaunchKernelGGL((gg_rows_kernel<EPI_SCATTER, false>), dim3(grid), dim3(kGemmThreads), 0, stream, a);
   else
     hipLaunchKernelGGL((gg_rows_kernel<EPI_SWIGLU_BWD, true>), dim3(grid), dim3(kGemmThreads), 0, stream, a);
   return hipGetLastError();
 }
 
+static hipError_t fwd(int epi, FwdGemm g, const int* offs, int E, int M, void* ws,
+                      hipStream_t stream) {
+  hipError_t err = launch_tile_map(offs, E, M, ws, stream);
+  if (err != hipSuccess) return err;
+  const TileTable tt = tile_table_in(ws);
+  g.table = tt.table;
+  g.n_qtiles = tt.count;
+  return launch_fwd_gemm(epi, g, stream);
+}
+
 hipError_t launch_grouped_mm(const void* x, const void* w, const int* offs, int M, int E,
                              int N, int K, void* out, void* ws, hipStream_t stream) {
-  RowsArgs a = {};
-  a.q = (const bf16_t*)x; a.ldq = K;
-  a.p = (const bf16_t*)w; a.p_estride = (int64_t)N * K; a.ldp = K;
-  a.kred = K; a.np_tiles = N / BP;
-  a.out = (bf16_t*)out; a.ldo = N;
-  return launch_rows(EPI_STORE, false, a, offs, E, M, ws, stream);
+  FwdGemm g = {};
+  g.act = x; g.w = w; g.kred = K; g.n = N; g.out = out;
+  return fwd(EPI_STORE, g, offs, E, M, ws, stream);
 }
 
 hipError_t launch_grouped_mm_swiglu(const void* x, const void* w13, const int* offs, int M,
                                     int E, int H, int D, float limit, void* a_out, void* h_out,
                                     void* ws, hipStream_t stream) {
-  RowsArgs a = {};
-  a.q = (const bf16_t*)x; a.ldq = D;
-  a.p = (const bf16_t*)w13; a.p_estride = (int64_t)2 * H * D; a.ldp = D;
-  a.kred = D; a.np_tiles = H / 64;
-  a.out = (bf16_t*)a_out; a.ldo = H;
-  a.hidden = H; a.limit = limit; a.h_out = (bf16_t*)h_out; a.ldh = 2 * (int64_t)H;
-  return launch_rows(EPI_SWIGLU, false, a, offs, E, M, ws, stream);
+  FwdGemm g = {};
+  g.act = x; g.w = w13; g.kred = D; g.n = H; g.out = a_out; g.limit = limit; g.h_out = h_out;
+  return fwd(EPI_SWIGLU, g, offs, E, M, ws, stream);
 }
 
 hipError_t launch_grouped_mm_unpermute(const void* act, const void* w2, const int* offs, int M,
                                        int E, int D, int H, const float* row_scale,
                                        const int* dest, int n_dest, void* out, void* ws,
                                        hipStream_t stream) {
-  RowsArgs a = {};
-  a.q = (const bf16_t*)act; a.ldq = H;
-  a.p = (const bf16_t*)w2; a.p_estride = (int64_t)D * H; a.ldp = H;
-  a.kred = H; a.np_tiles = D / BP;
-  a.out = (bf16_t*)out; a.ldo = D;
-  a.row_scale = row_scale; a.dest = dest; a.n_dest = n_dest;
-  return launch_rows(EPI_SCATTER, false, a, offs, E, M, ws, stream);
+  FwdGemm g = {};
+  g.act = act; g.w = w2; g.kred = H; g.n = D; g.out = out;
+  g.row_scale = row_scale; g.dest = dest; g.n_dest = n_dest;
+  return fwd(EPI_SCATTER, g, offs, E, M, ws, stream);
 }
 
 hipError_t launch_grouped_mm_dgrad(const void* dy, const void* w, const int* offs, int M, int E,

@@ -1,0 +1,61 @@
+// Pieces shared by the grouped GEMM kernels (internal to libttamd_moe.so).
+#pragma once
+
+#include "common.h"
+
+namespace ttamd {
+
+// Epilogue variants of the token-row GEMMs.
+enum Epi {
+  EPI_STORE = 0,       // out[q][p] = acc
+  EPI_SWIGLU = 1,      // gate/up pairs -> silu(clamp(gate)) * clamp(up)
+  EPI_SCATTER = 2,     // out[dest[q]][p] = scale[q] * acc
+  EPI_SWIGLU_BWD = 3,  // dh from dA = acc and the saved pre-activation h
+};
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
+
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+// Token-row tiles of 128 rows: table[i] = {expert, first row, end row, 0}.
+constexpr int kTileRows = 128;
+
+// Workspace of a token-row GEMM: int4 header {number of tiles, ...} followed
+// by the tile table.
+struct TileTable {
+  int* count;
+  int4* table;
+};
+
+inline int max_row_tiles(int M, int E) { return M / kTileRows + E + 1; }
+
+inline TileTable tile_table_in(void* ws) {
+  TileTable t;
+  t.count = (int*)ws;
+  t.table = (int4*)ws + 1;
+  return t;
+}
+
+// Forward GEMM description (gemm_fwd.hip).
+//   act [M][kred] bf16, w [E][N or 2N][kred] bf16.
+//   EPI_SWIGLU: n = H (w holds 2H rows: gate then up), out [M][H], h_out [M][2H].
+//   EPI_STORE / EPI_SCATTER: n = N, out [M or n_dest][N].
+struct FwdGemm {
+  const void* act;
+  const void* w;
+  int kred;
+  int n;
+  const int4* table;
+  const int* n_qtiles;
+  void* out;
+  float limit;
+  void* h_out;
+  const float* row_scale;
+  const int* dest;
+  int n_dest;
+};
+
+hipError_t launch_tile_map(const int* offs, int E, int M, void* ws, hipStream_t stream);
+hipError_t launch_fwd_gemm(int epi, const FwdGemm& g, hipStream_t stream);
+
+}  // namespace ttamd
