@@ -43,22 +43,30 @@ __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r ^ (r >> 2)) & 
 __device__ __forceinline__ int lds_off(int r, int c) { return r * BK + swz(r, c) * 8; }
 
 // ---------------------------------------------------------------------------
-// Tile table: q-tile i -> {expert, first row, end row}.  Built on the device
-// from the inclusive group offsets, so no count ever reaches the host.
+// Tile table: token tile i -> {expert, first row, end row}.  Built on the
+// device from the inclusive group offsets, so no count reaches the host.
+// An expert's rows are split into the fewest tiles of at most max_rows rows,
+// of equal height rounded up to 32 rows (540 rows at max_rows = 256 give
+// 3 tiles of 192 rather than 256 + 256 + 28).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void tile_map_kernel(const int* __restrict__ offs, int E,
-                                                        int M, int max_tiles,
+                                                        int M, int max_tiles, int max_rows,
                                                         int4* __restrict__ table,
                                                         int* __restrict__ count) {
   __shared__ int wave_sums[16];
   const int tid = threadIdx.x;
-  int r0 = 0, r1 = 0, nt = 0;
+  int r0 = 0, r1 = 0, nt = 0, h = max_rows;
   if (tid < E) {
     const int a = (tid == 0) ? 0 : offs[tid - 1];
     const int b = offs[tid];
     r0 = min(max(a, 0), M);
     r1 = min(max(b, r0), M);
-    nt = (r1 - r0 + BQ - 1) / BQ;
+    const int c = r1 - r0;
+    if (c > 0) {
+      const int n0 = (c + max_rows - 1) / max_rows;
+      h = (((c + n0 - 1) / n0) + 31) & ~31;
+      nt = (c + h - 1) / h;
+    }
   }
   const int incl = wave_inclusive_scan(nt);
   const int w = tid / kWave, l = lane_id();
@@ -74,16 +82,16 @@ __global__ __launch_bounds__(1024) void tile_map_kernel(const int* __restrict__ 
   const int total = wave_sums[15];
   for (int t = 0; t < nt; ++t) {
     const int i = start + t;
-    if (i < max_tiles) table[i] = make_int4(tid, r0 + t * BQ, min(r0 + (t + 1) * BQ, r1), 0);
+    if (i < max_tiles) table[i] = make_int4(tid, r0 + t * h, min(r0 + (t + 1) * h, r1), 0);
   }
   for (int i = total + tid; i < max_tiles; i += 1024) table[i] = make_int4(-1, 0, 0, 0);
   if (tid == 0) *count = min(total, max_tiles);
 }
 
-hipError_t launch_tile_map(const int* offs, int E, int M, void* ws, hipStream_t stream) {
+hipError_t launch_tile_map(const int* offs, int E, int M, int max_rows, void* ws, hipStream_t stream) {
   TileTable tt = tile_table_in(ws);
   hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, stream, offs, E, M,
-                     max_row_tiles(M, E), tt.table, tt.count);
+                     max_row_tiles(M, E), max_rows, tt.table, tt.count);
   return hipGetLastError();
 }
 
@@ -521,7 +529,7 @@ static int round_up8(int x) { return (x + 7) & ~7; }
 static hipError_t launch_rows(int epi, bool ptrans, RowsArgs a, const int* offs, int E, int M,
                               void* ws, hipStream_t stream) {
   const int max_q = gemm_max_qtiles(M, E);
-  hipError_t err = launch_tile_map(offs, E, M, ws, stream);
+  hipError_t err = launch_tile_map(offs, E, M, BQ, ws, stream);
   if (err != hipSuccess) return err;
   a.table = tile_table_in(ws).table;
   a.max_qtiles = max_q;
@@ -538,7 +546,7 @@ static hipError_t launch_rows(int epi, bool ptrans, RowsArgs a, const int* offs,
 
 static hipError_t fwd(int epi, FwdGemm g, const int* offs, int E, int M, void* ws,
                       hipStream_t stream) {
-  hipError_t err = launch_tile_map(offs, E, M, ws, stream);
+  hipError_t err = launch_tile_map(offs, E, M, kFwdTileRows, ws, stream);
   if (err != hipSuccess) return err;
   const TileTable tt = tile_table_in(ws);
   g.table = tt.table;

@@ -17,8 +17,11 @@ __device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x))
 
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
-// Token-row tiles of 128 rows: table[i] = {expert, first row, end row, 0}.
+// Token-row tiles: table[i] = {expert, first row, end row, 0}, at most
+// kFwdTileRows rows for the forward GEMM, 128 for the dgrad GEMM.  The
+// workspace is sized for the smaller tiles (more of them).
 constexpr int kTileRows = 128;
+constexpr int kFwdTileRows = 256;
 
 // Workspace of a token-row GEMM: int4 header {number of tiles, ...} followed
 // by the tile table.
@@ -55,7 +58,36 @@ struct FwdGemm {
   int n_dest;
 };
 
-hipError_t launch_tile_map(const int* offs, int E, int M, void* ws, hipStream_t stream);
+// Kernel arguments of the forward GEMMs (gemm_fwd.hip, gemm_ring.hip).
+struct FwdArgs {
+  const bf16_t* q;  // activations [M][kred]
+  int64_t ldq;
+  const bf16_t* p;  // weights, expert e at p + e * p_estride, rows of ldp
+  int64_t p_estride;
+  int64_t ldp;
+  int kred;
+  int n_p;       // valid weight rows (SWIGLU: H, the gate half)
+  int np_tiles;  // weight-row tiles per token tile
+  const int4* table;
+  const int* n_qtiles;
+  bf16_t* out;
+  int64_t ldo;
+  // EPI_SWIGLU
+  int64_t hidden;
+  float limit;  // NaN = no clamp
+  bf16_t* h_out;
+  int64_t ldh;
+  // EPI_SCATTER
+  const float* row_scale;
+  const int* dest;
+  int n_dest;
+};
+
+int num_cus();
+
+hipError_t launch_tile_map(const int* offs, int E, int M, int max_rows, void* ws,
+                           hipStream_t stream);
+// Forward GEMM over a tile table of at most kFwdTileRows rows per tile.
 hipError_t launch_fwd_gemm(int epi, const FwdGemm& g, hipStream_t stream);
 
 }  // namespace ttamd
