@@ -49,7 +49,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=2048, help="token sample for the CPU oracle baseline")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 256 MiB device copy (reference for the PMC byte counters) and exit")
+    ap.add_argument("--cpu-tokens", type=int, default=2048, help="unused (kept for old command lines)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum CPU time of the oracle baseline")
     return ap.parse_args()
 
 
@@ -65,6 +68,16 @@ def main():
         sys.exit(2)
     import numpy as np
     import torch
+
+    if args.calibrate_copy:
+        n = 256 << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": n, "launches": 3}), flush=True)
+        return
 
     ops = importlib.import_module("torchtitan-ascend_amd.ops")
     F = importlib.import_module("torchtitan-ascend_amd.functional")
@@ -98,9 +111,18 @@ def main():
         logits = torch.matmul(x, w_router.t())  # upstream router gate (nn.Linear, bf16)
         return ops.router_topk(logits, K, cfg["router"], cfg["norm"])
 
-    def step_forward():
-        scores, idx = router()
-        return F.moe_experts_forward(x, scores, idx, w13, w2, E, cfg["score_before"])
+    def timed_router(ev):
+        if ev is None:
+            return router()
+        pair = ev.setdefault("router", (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)))
+        pair[0].record()
+        out = router()
+        pair[1].record()
+        return out
+
+    def step_forward(ev=None):
+        scores, idx = timed_router(ev)
+        return F.moe_experts_forward(x, scores, idx, w13, w2, E, cfg["score_before"], stage_events=ev)
 
     if cfg["backward"]:
         w13p = w13.clone().requires_grad_(True)
@@ -108,67 +130,52 @@ def main():
         dout = torch.randn(T, D, device=dev).to(torch.bfloat16)
         xg = x.clone().requires_grad_(True)
 
-        def step():
+        def step(ev=None):
             scores, idx = router()
             scores = scores.detach().requires_grad_(True)
             out = F.moe_experts_forward(xg, scores, idx, w13p, w2p, E, cfg["score_before"])
             out.backward(dout)
             return out
     else:
-        def step():
+        def step(ev=None):
             with torch.no_grad():
-                return step_forward()
+                return step_forward(ev)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     log("warmup done")
+    # Timed region: K steps between two synchronisations.  Each step records
+    # an event pair around every stage on the stream its kernels run on (the
+    # current stream), so the per-stage and dominant-kernel durations are
+    # measured live over the same steps.
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    step_events = []
     torch.cuda.synchronize()
     start.record()
     for _ in range(args.steps):
-        step()
+        ev = {}
+        step(ev)
+        step_events.append(ev)
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
     log(f"timed {args.steps} steps: {ms:.3f} ms/step")
 
-    # ---- per-stage breakdown and the dominant kernel, timed live --------------
-    with torch.no_grad():
-        scores, idx = router()
-        r = ops.route(idx, E, scores.reshape(-1).float())
-        routed = ops.gather_rows(x, r.sorted_indices, K, r.sorted_scores if cfg["score_before"] else None)
-        a, _ = ops.grouped_mm_swiglu(routed, w13, r.offs)
-        scale = None if cfg["score_before"] else r.sorted_scores
-
-        def w2_stage():
-            if K == 1:
-                return ops.grouped_mm_unpermute(a, w2, r.offs, scale, r.sorted_indices, T)
-            return ops.grouped_mm_unpermute(a, w2, r.offs, scale, r.sorted_indices, M)
-
-        ybuf = w2_stage()
-        stages = {
-            "router": lambda: router(),
-            "route": lambda: ops.route(idx, E, scores.reshape(-1).float()),
-            "permute": lambda: ops.gather_rows(x, r.sorted_indices, K,
-                                               r.sorted_scores if cfg["score_before"] else None),
-            "gemm_w13_swiglu": lambda: ops.grouped_mm_swiglu(routed, w13, r.offs),
-            "gemm_w2_unpermute": w2_stage,
-        }
-        if K > 1:
-            stages["sum_topk"] = lambda: ops.sum_topk(ybuf, K)
-        reps = 20
-        stage_us = {}
-        for name, fn in stages.items():
-            fn()
+    stage_us = {}
+    if step_events and step_events[0]:
+        for name in step_events[0]:
+            vals = [e[name][0].elapsed_time(e[name][1]) * 1000.0 for e in step_events]
+            stage_us[name] = sum(vals) / len(vals)
+    else:
+        # training configs: stage breakdown from extra no-grad forward passes
+        for _ in range(3):
+            ev = {}
+            with torch.no_grad():
+                step_forward(ev)
             torch.cuda.synchronize()
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            for _ in range(reps):
-                fn()
-            e.record()
-            torch.cuda.synchronize()
-            stage_us[name] = s.elapsed_time(e) * 1000.0 / reps
+            for name, (s0, s1) in ev.items():
+                stage_us[name] = stage_us.get(name, 0.0) + s0.elapsed_time(s1) * 1000.0 / 3
     log(f"stages (us): {json.dumps({k: round(v, 1) for k, v in stage_us.items()})}")
 
     w13_flops = 4.0 * M * D * H
@@ -176,6 +183,7 @@ def main():
     gemm_us = stage_us["gemm_w13_swiglu"] + stage_us["gemm_w2_unpermute"]
     gemm_tflops = (w13_flops + w2_flops) / (gemm_us * 1e-6) / 1e12
     w13_tflops = w13_flops / (stage_us["gemm_w13_swiglu"] * 1e-6) / 1e12
+    w2_tflops = w2_flops / (stage_us["gemm_w2_unpermute"] * 1e-6) / 1e12
     permute_bytes = T * D * 2 + M * D * 2 + 8 * M
     permute_gbs = permute_bytes / (stage_us["permute"] * 1e-6) / 1e9
 
@@ -201,17 +209,19 @@ def main():
         "layer_tflops": round(total_flops / (ms * 1e-3) / 1e12, 1),
         "grouped_gemm_tflops": round(gemm_tflops, 1),
         "grouped_gemm_frac_of_peak": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
+        "gemm_w13_tflops": round(w13_tflops, 1),
+        "gemm_w2_tflops": round(w2_tflops, 1),
         "permute_gbs": round(permute_gbs, 1),
         "permute_frac_of_hbm": round(permute_gbs / PEAK_HBM_GBS, 4),
         "stage_us": {k: round(v, 2) for k, v in stage_us.items()},
         "roofline": {
-            "kernel": "gg_rows_kernel<EPI_SWIGLU> (grouped GEMM w13 + SwiGLU)",
+            "kernel": "gg_fwd_kernel<EPI_SWIGLU> (grouped GEMM w13 + SwiGLU epilogue)",
             "bound": "mfma",
             "achieved": round(w13_tflops, 1),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(w13_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.config),
             "algorithmic_flops_per_launch": w13_flops,
             "avg_launch_us": round(stage_us["gemm_w13_swiglu"], 2),
         },
@@ -220,6 +230,18 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, cfg, x, w13, w2, router)
     print(json.dumps(result), flush=True)
+
+
+def measured_traffic(config):
+    """HBM bytes per launch of the w13 kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary of this workload (null when absent)."""
+    path = ROOT / "profiles" / f"gg_fwd_swiglu_{config}_hbm_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def cpu_baseline(args, cfg, x, w13, w2, router):
@@ -235,18 +257,26 @@ def cpu_baseline(args, cfg, x, w13, w2, router):
         threads = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"), default=1)
     except Exception:  # pragma: no cover
         threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
-    Ts = min(args.cpu_tokens, cfg["T"])
+    Tfull = cfg["T"]
     with torch.no_grad():
         scores, idx = router()
-    xs = x[:Ts].float().cpu().numpy()
-    ss = scores[:Ts].float().cpu().numpy()
-    ix = idx[:Ts].cpu().numpy()
+    xs_all = x.float().cpu().numpy()
+    ss_all = scores.float().cpu().numpy()
+    ix_all = idx.cpu().numpy()
     w13n = w13.float().cpu().numpy()
     w2n = w2.float().cpu().numpy()
-    log(f"cpu baseline: oracle on {Ts} tokens, {threads} BLAS threads")
+    # warm-up on a small slice, then whole-workload passes until >= cpu_seconds
+    O.moe_forward(xs_all[:256], ss_all[:256], ix_all[:256], w13n, w2n, cfg["E"], cfg["score_before"])
+    log(f"cpu baseline: oracle forward on {Tfull} tokens per pass, {threads} BLAS threads")
     t0 = time.perf_counter()
-    O.moe_forward(xs, ss, ix, w13n, w2n, cfg["E"], cfg["score_before"])
-    dt = time.perf_counter() - t0
+    passes = 0
+    while True:
+        O.moe_forward(xs_all, ss_all, ix_all, w13n, w2n, cfg["E"], cfg["score_before"])
+        passes += 1
+        dt = time.perf_counter() - t0
+        if dt >= args.cpu_seconds or passes >= 50:
+            break
+    Ts = Tfull * passes
     try:
         model = [ln.split(":", 1)[1].strip() for ln in open("/proc/cpuinfo") if ln.startswith("model name")][0]
     except Exception:  # pragma: no cover
@@ -256,8 +286,8 @@ def cpu_baseline(args, cfg, x, w13, w2, router):
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{Ts} of {cfg['T']} tokens of the same workload (forward), oracle.moe_oracle.moe_forward, "
-                  f"{dt:.2f} s on {model}",
+        "sample": f"{passes} pass(es) of the full workload forward ({Tfull} tokens each, same inputs and routing) "
+                  f"through oracle.moe_oracle.moe_forward (numpy fp32): {dt:.2f} s on {model}",
     }
 
 

@@ -7,39 +7,37 @@
 // epilogue, for the w2 down-projection with the routing-weight scale and the
 // un-permute scatter fused into the epilogue, and for the plain grouped GEMM.
 //
-// Tile: up to 256 token rows (Q) x 256 weight rows (P); k in stages of 32.
+// Tile: up to 256 token rows (Q) x 256 weight rows (P); k in stages of 64.
 //   * 4 waves, one per SIMD, in a 2 x 2 arrangement: wave (wq, wp) owns
 //     token rows 128wq.. and 128 weight rows, i.e. 4 x 4 accumulators of
 //     v_mfma_f32_32x32x16_bf16 (256 fp32 AGPRs per lane).  The MFMA A
 //     operand is the weight tile, B the token tile, so a lane holds 4
 //     consecutive output columns per register group.  SWIGLU: a wave's weight
 //     rows are 64 gate rows and the 64 matching up rows.
-//   * Five LDS stage buffers of 32 KB (16 KB weights + 16 KB tokens, rows of
-//     64 bytes) filled by global_load_lds_dwordx4 (HBM/L2 -> LDS without VGPR
-//     staging), four stages ahead: 128 KB in flight per CU.  The 16-byte
-//     chunk c of row r sits at c ^ (((r >> 2) ^ (r >> 1)) & 3), conflict-free
-//     for the 16 consecutive rows a fragment read serves per LDS cycle.  A
-//     wave's DMA writes 1 KB of LDS contiguously, so the permutation is
-//     applied to the global addresses.
-//   * MFMA fragments are read one k16 step ahead; the barrier for stage
-//     s + 1 sits between the two k16 steps of stage s, after the last reads
-//     of stage s, so stage s's buffer takes the DMA of stage s + 5 at once.
+//   * Two LDS stage buffers of 64 KB (32 KB weights + 32 KB tokens, rows of
+//     128 bytes = one full cache line per row and stage) filled by
+//     global_load_lds_dwordx4 (HBM/L2 -> LDS without VGPR staging).  A DMA
+//     instruction moves 8 whole rows; half-line rows (k stages of 32) cost
+//     twice the L2 requests per byte and capped the load rate.  The 16-byte
+//     chunk c of row r sits at c ^ ((r ^ (r >> 3)) & 7): the 8 (and 16)
+//     consecutive rows a fragment read serves per LDS cycle hit distinct
+//     banks.  A wave's DMA writes 1 KB of LDS contiguously, so the
+//     permutation is applied to the global addresses.
+//   * MFMA fragments are read one k16 step ahead; the single barrier of a
+//     stage sits before its last k16 step, after the last reads of the stage,
+//     and is where the next-but-one stage is issued into the freed buffer.
 //   * Per tile, a wave-uniform byte base (SGPRs) plus one 32-bit per-lane
 //     offset per DMA instruction; per stage only the k offset changes.
 //   * Persistent: one workgroup per CU walks the tile list with stride
 //     gridDim.x; the DMA stream runs over the flattened (tile, k-stage)
 //     sequence, so the next tile's first stages load during the current
-//     tile's last ones.  Within a round the 32 workgroups of one XCD take 32
+//     tile's epilogue.  Within a round the 32 workgroups of one XCD take 32
 //     consecutive tiles (same expert), so the weights are shared in its L2.
-//   * Tiles shorter than 256 rows (expert tails) skip the MFMAs of the
-//     32-row token blocks they do not have (per-wave specialisation).
 //
 // Reference semantics (torchtitanturbo/models/common/npu_gmm.py):
 //   :17-18, :31, :38  torch._grouped_mm(x, w.transpose(-2, -1), offs)
 //   :32-36            optional clamp with swiglu_limit
 //   :37               npu_swiglu: silu(gate) * up, gate = first H columns
-#include <type_traits>
-
 #include "common.h"
 #include "gemm_common.h"
 #include "kernels.h"
@@ -49,13 +47,18 @@ namespace {
 
 constexpr int TQ = kFwdTileRows;  // 256 token rows
 constexpr int TP = 256;           // weight rows
-constexpr int TK = 32;            // k per stage
-constexpr int NSTAGE = 5;
+constexpr int NJ = TQ / 64;       // 32-row token blocks per wave
+constexpr int TK = 64;            // k per stage: 128-byte rows
+constexpr int NSTAGE = 2;
 constexpr int FTHREADS = 256;
-constexpr int P_BYTES = TP * TK * 2;                   // 16 KB
-constexpr int STAGE_BYTES = P_BYTES + TQ * TK * 2;     // 32 KB
-constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;        // 160 KB
-constexpr int DMA_PER_STAGE = STAGE_BYTES / 16 / FTHREADS;  // 8 per lane
+constexpr int ROW_BYTES = TK * 2;
+constexpr int P_BYTES = TP * ROW_BYTES;                // 32 KB
+constexpr int STAGE_BYTES = P_BYTES + TQ * ROW_BYTES;  // 64 KB
+constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;        // 128 KB
+constexpr int DMA_P = TP / 8 / 4;                      // 8 weight-row instructions per wave
+constexpr int DMA_Q = TQ / 8 / 4;                      // 8 token-row instructions per wave
+constexpr int DMA_PER_STAGE = DMA_P + DMA_Q;           // 16 per lane
+static_assert(TQ % 64 == 0 && TP == 256, "tile geometry");
 
 typedef __attribute__((address_space(3))) char* lds_ptr_t;
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
@@ -64,8 +67,8 @@ __device__ __forceinline__ uint32_t lds_addr(const char* p) {
   return (uint32_t)(uintptr_t)(lds_ptr_t)p;
 }
 
-// Chunk permutation of 64-byte LDS rows.
-__device__ __forceinline__ int cswz(int r) { return ((r >> 2) ^ (r >> 1)) & 3; }
+// Chunk permutation of 128-byte LDS rows.
+__device__ __forceinline__ int cswz(int r) { return (r ^ (r >> 3)) & 7; }
 
 // ---------------------------------------------------------------------------
 // Memory operations the compiler must not track or move.
@@ -73,11 +76,10 @@ __device__ __forceinline__ int cswz(int r) { return ((r >> 2) ^ (r >> 1)) & 3; }
 // The LDS DMA loads, the stage barrier and the tile-table loads are inline
 // asm: the compiler neither tracks the DMA (with DMA and other loads in
 // flight it would wait for everything before each LDS read) nor moves
-// memory operations across them ("memory" clobber).  The kernel counts its
-// own vector-memory operations: every stage issues exactly DMA_PER_STAGE
-// DMAs per lane (stages past the end re-load the last stage), and vector
-// memory operations of a wave complete in issue order, so "at most N in
-// flight" means "all but the N most recent have completed".
+// memory operations across them ("memory" clobber).  At each stage barrier
+// exactly one stage is in flight and the kernel waits for all of its vector
+// memory operations (vmcnt(0)), which also covers the epilogue's loads and
+// stores.
 //
 // GFX9-family manual wait states the compiler cannot see through inline asm:
 // a VMEM/SMEM instruction reading an SGPR written by a VALU instruction
@@ -132,10 +134,10 @@ __device__ __forceinline__ int sload_int(const int* p) {
   return __builtin_amdgcn_readfirstlane(v);
 }
 
-// MFMA fragments of one k16 step: 4 weight blocks, 4 token blocks.
+// MFMA fragments of one k16 step: 4 weight blocks, NJ token blocks.
 struct Frag {
   bf16x8_t a[4];
-  bf16x8_t b[4];
+  bf16x8_t b[NJ];
 };
 
 template <int EPI>
@@ -157,11 +159,10 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   if (total == 0) return;
 
   const uint32_t lds0 = lds_addr(smem);
-  // DMA lane geometry: instruction i of wave w writes rows 16 * (4i + w) +
-  // l / 4, physical chunk l % 4, whose logical chunk is l % 4 ^ cswz(row);
-  // cswz(row) only depends on l.
-  const int drow = l >> 2;
-  const int dchunk = (l & 3) ^ (((l >> 4) ^ (l >> 3)) & 3);
+  // DMA lane geometry: instruction i of wave w (per operand) writes the 8
+  // rows of row block rb = 4i + w, row 8rb + l / 8, physical chunk l % 8,
+  // whose logical chunk is l % 8 ^ cswz(row) = l % 8 ^ ((l / 8 ^ rb) & 7).
+  const int drow = l >> 3;
 
   // ---- DMA stream -----------------------------------------------------------
   int d_r = -1;  // tile round whose addresses are loaded
@@ -173,9 +174,12 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     const int pt = tile - qt * a.np_tiles;
     const int4 ti = sload_int4(a.table + qt);
     const int64_t ldp2 = a.ldp * 2;
+    const int qmax = ti.z - ti.y - 1;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rr = 16 * (4 * i + w) + drow;  // tile weight row 0..255
+    for (int i = 0; i < DMA_P; ++i) {
+      const int rb = 4 * i + w;
+      const int rr = 8 * rb + drow;  // tile weight row 0..255
+      const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
       int prow;
       if constexpr (EPI == EPI_SWIGLU) {
         const int col = min(pt * 128 + (rr & 127), a.n_p - 1) - pt * 128;
@@ -183,19 +187,20 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
       } else {
         prow = min(pt * TP + rr, a.n_p - 1) - pt * TP;
       }
-      d_voff[i] = (uint32_t)(prow * ldp2 + dchunk * 16);
+      d_voff[i] = (uint32_t)(prow * ldp2 + lchunk * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < DMA_Q; ++i) {
+      const int rb = 4 * i + w;
+      const int rr = 8 * rb + drow;  // tile token row 0..TQ-1
+      const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
+      d_voff[DMA_P + i] = (uint32_t)(min(rr, qmax) * a.ldq * 2 + lchunk * 16);
     }
     if constexpr (EPI == EPI_SWIGLU)
       d_pbase = (uint64_t)(a.p + (int64_t)ti.x * a.p_estride + (int64_t)pt * 128 * a.ldp);
     else
       d_pbase = (uint64_t)(a.p + (int64_t)ti.x * a.p_estride + (int64_t)pt * TP * a.ldp);
     d_qbase = (uint64_t)(a.q + (int64_t)ti.y * a.ldq);
-    const int qmax = ti.z - ti.y - 1;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rr = 16 * (4 * i + w) + drow;  // tile token row 0..255
-      d_voff[4 + i] = (uint32_t)(min(rr, qmax) * a.ldq * 2 + dchunk * 16);
-    }
     d_r = r;
   };
   auto issue = [&](int s) {
@@ -203,89 +208,127 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     const int r = sc / ksteps;
     const int ks = sc - r * ksteps;
     if (r != d_r) dma_tile(r);
-    const uint64_t pb = d_pbase + (uint64_t)ks * (TK * 2);
-    const uint64_t qb = d_qbase + (uint64_t)ks * (TK * 2);
-    const uint32_t st = lds0 + (uint32_t)((s % NSTAGE) * STAGE_BYTES) + w * 1024;
+    const uint64_t pb = d_pbase + (uint64_t)ks * ROW_BYTES;
+    const uint64_t qb = d_qbase + (uint64_t)ks * ROW_BYTES;
+    const uint32_t st = lds0 + (uint32_t)((s & 1) * STAGE_BYTES) + w * 1024;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(d_voff[i], pb, st + i * 4096);
+    for (int i = 0; i < DMA_P; ++i) dma16(d_voff[i], pb, st + i * 4096);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(d_voff[4 + i], qb, st + P_BYTES + i * 4096);
+    for (int i = 0; i < DMA_Q; ++i) dma16(d_voff[DMA_P + i], qb, st + P_BYTES + i * 4096);
   };
 
   // ---- fragment geometry -------------------------------------------------------
+  // Row 32m + r32 has cswz = fa ^ 4 * (m & 1) with fa = cswz(r32); all
+  // fragment blocks start at multiples of 32 rows.
   const int r32 = l & 31;
   const int half = l >> 5;
-  const int fs = cswz(r32);  // cswz(32m + r32) == cswz(r32)
+  const int fa = cswz(r32);
   int arow[4];
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb)
     arow[pb] = (EPI == EPI_SWIGLU) ? (pb < 2 ? 64 * wp + 32 * pb : 128 + 64 * wp + 32 * (pb - 2))
                                    : 128 * wp + 32 * pb;
   auto read_frag = [&](Frag& f, int s, int kk) {
-    const bf16_t* st = (const bf16_t*)(smem + (s % NSTAGE) * STAGE_BYTES);
-    const int pc = (((2 * kk + half) ^ fs) * 8);
+    const char* st = smem + (s & 1) * STAGE_BYTES;
 #pragma unroll
-    for (int pb = 0; pb < 4; ++pb) f.a[pb] = *(const bf16x8_t*)(st + (arow[pb] + r32) * TK + pc);
+    for (int pb = 0; pb < 4; ++pb) {
+      const int pc = (2 * kk + half) ^ fa ^ (4 * ((arow[pb] >> 5) & 1));
+      f.a[pb] = *(const bf16x8_t*)(st + (arow[pb] + r32) * ROW_BYTES + pc * 16);
+    }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      f.b[j] = *(const bf16x8_t*)(st + P_BYTES / 2 + (128 * wq + 32 * j + r32) * TK + pc);
+    for (int j = 0; j < NJ; ++j) {
+      const int m = NJ * wq + j;  // 32-row token block
+      const int pc = (2 * kk + half) ^ fa ^ (4 * (m & 1));
+      f.b[j] = *(const bf16x8_t*)(st + P_BYTES + (32 * m + r32) * ROW_BYTES + pc * 16);
+    }
   };
 
-  // ---- prologue: stages 0..4 in flight, fragments of stage 0 / k16 0 read ----
-#pragma unroll
-  for (int s0 = 0; s0 < NSTAGE; ++s0) issue(s0);
-  wait_vm_barrier<(NSTAGE - 1) * DMA_PER_STAGE>();
+  // ---- prologue: stages 0 and 1 in flight, fragments of stage 0 / k16 0 read --
+  issue(0);
+  issue(1);
+  wait_vm_barrier<DMA_PER_STAGE>();
   Frag f0, f1;
   read_frag(f0, 0, 0);
 
   int s = 0;
-  auto run_tile = [&](auto nqb_tag, int row0, int row1, int pt) {
-    constexpr int NQB = decltype(nqb_tag)::value;  // this wave's 32-row token blocks
-    floatx16_t acc[4][NQB > 0 ? NQB : 1];
+  auto run_tile = [&](int row0, int row1, int pt) {
+    floatx16_t acc[4][NJ];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < (NQB > 0 ? NQB : 1); ++j)
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
     auto mfma = [&](const Frag& f) {
 #pragma unroll
-      for (int j = 0; j < NQB; ++j)
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
         for (int pb = 0; pb < 4; ++pb)
           acc[pb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[pb], f.b[j], acc[pb][j], 0, 0, 0);
     };
+    // Per-row epilogue operands, loaded while the tile's k loop runs.  The
+    // compiler cannot see the DMA counts, so it would wait for every memory
+    // operation before their first use; touching them right after each stage
+    // barrier (where nothing is in flight) puts that wait where it is free.
+    int dst[NJ];
+    float rsc[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int gq = row0 + NJ * 32 * wq + 32 * j + r32;
+      dst[j] = gq;
+      rsc[j] = 1.f;
+      if constexpr (EPI == EPI_SCATTER) {
+        const bool row_ok = gq < row1;
+        if (a.dest) dst[j] = row_ok ? a.dest[gq] : 0;  // clamped at use
+        if (a.row_scale) rsc[j] = row_ok ? a.row_scale[gq] : 0.f;
+      }
+    }
 
-    // One stage: k16 step 0 from f0 while step 1 is read into f1; the
-    // barrier for stage s + 1 between the two steps.  Stage s + 1 has landed
-    // once only the DMAs of stages s + 2 .. s + 4 may be in flight, and
-    // every wave has finished its reads of stage s (its buffer is refilled).
+    // One stage: k16 steps 0..3, each computed from registers while the next
+    // is read.  Before step 3 every wave has read all of stage s; the barrier
+    // there also waits for stage s + 1 (the only stage in flight), and stage
+    // s + 2 is issued into stage s's buffer.
+    auto touch_epilogue_operands = [&]() {
+      if constexpr (EPI == EPI_SCATTER) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) asm volatile("" ::"v"(dst[j]), "v"(rsc[j]));
+      }
+    };
     for (int ks = 0; ks + 1 < ksteps; ++ks, ++s) {
       read_frag(f1, s, 1);
       mfma(f0);
-      wait_vm_barrier<3 * DMA_PER_STAGE>();
-      issue(s + NSTAGE);
+      read_frag(f0, s, 2);
+      mfma(f1);
+      read_frag(f1, s, 3);
+      mfma(f0);
+      wait_vm_barrier<0>();
+      touch_epilogue_operands();
+      issue(s + 2);
       read_frag(f0, s + 1, 0);
       mfma(f1);
     }
     // Last stage of the tile: the next tile's first fragments are read after
-    // the epilogue (fewer live registers there); stage s + 1's buffer is not
-    // refilled before the next barrier.
+    // the epilogue (fewer live registers there).
     read_frag(f1, s, 1);
     mfma(f0);
-    wait_vm_barrier<3 * DMA_PER_STAGE>();
-    issue(s + NSTAGE);
+    read_frag(f0, s, 2);
+    mfma(f1);
+    read_frag(f1, s, 3);
+    mfma(f0);
+    wait_vm_barrier<0>();
+    touch_epilogue_operands();
+    issue(s + 2);
     mfma(f1);
     ++s;
 
-    // ---- epilogue: acc[pb][j][4g + i] is (token row 128wq + 32j + r32,
+    // ---- epilogue: acc[pb][j][4g + i] is (token row NJ*32wq + 32j + r32,
     //      weight row arow[pb] + 8g + 4 * half + i).  Column validity is
     //      wave-uniform (H % 64 == 0 and N % 128 == 0 are required), row
     //      validity is per lane.  The scheduling barriers keep each block's
     //      accumulator reads next to their use (no 256-register hoist).
 #pragma unroll
-    for (int j = 0; j < NQB; ++j) {
-      const int gq = row0 + 128 * wq + 32 * j + r32;
+    for (int j = 0; j < NJ; ++j) {
+      const int gq = row0 + NJ * 32 * wq + 32 * j + r32;
       const bool row_ok = gq < row1;
       if constexpr (EPI == EPI_SWIGLU) {
         const bool clamp = (a.limit == a.limit);
@@ -324,13 +367,12 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
           }
         }
       } else {
-        int64_t orow_idx = gq;
-        float sc = 1.f;
+        const float sc = rsc[j];
+        int orow_idx = dst[j];
         if constexpr (EPI == EPI_SCATTER) {
-          if (a.dest) orow_idx = row_ok ? min(max(a.dest[gq], 0), a.n_dest - 1) : 0;
-          if (a.row_scale) sc = row_ok ? a.row_scale[gq] : 0.f;
+          if (a.dest) orow_idx = min(max(orow_idx, 0), a.n_dest - 1);
         }
-        bf16_t* orow = a.out + orow_idx * a.ldo;
+        bf16_t* orow = a.out + (int64_t)orow_idx * a.ldo;
 #pragma unroll
         for (int pb = 0; pb < 4; ++pb) {
           if (pt * TP + arow[pb] < a.n_p) {
@@ -355,8 +397,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     const int qt = tile / a.np_tiles;
     const int pt = tile - qt * a.np_tiles;
     const int4 ti = sload_int4(a.table + qt);
-    // this wave's token blocks: rows 128wq .. 128wq + 127 of the tile
-    run_tile(std::integral_constant<int, 4>{}, ti.y, ti.z, pt);
+    run_tile(ti.y, ti.z, pt);
   }
   wait_vm<0>();  // DMAs past the end have landed before the workgroup exits
 }

@@ -161,30 +161,55 @@ def moe_experts_forward(
     num_experts: int,
     score_before_experts: bool,
     swiglu_limit: float | None = None,
+    stage_events: dict | None = None,
 ) -> torch.Tensor:
     """dispatch -> experts -> combine for one GPU; x [T, D], scores/indices [T, K] -> [T, D].
 
     With autograd off (or nothing requiring grad) the score multiply and the
-    un-permute are fused into the w2 GEMM epilogue.
+    un-permute are fused into the w2 GEMM epilogue.  ``stage_events``, when
+    given (inference path only), receives a (start, end) pair of
+    torch.cuda.Event per stage, recorded on the current stream around the
+    stage's kernels: {"route", "permute", "gemm_w13_swiglu",
+    "gemm_w2_unpermute", "sum_topk"}.
     """
     T, D = x.shape
     K = top_scores.shape[-1]
-    scores_flat = top_scores.reshape(-1).float()
-    r = ops.route(selected_experts_indices, num_experts, scores_flat)
-    offs = r.offs
-    xb = x.to(_BF16).contiguous()
     training = torch.is_grad_enabled() and any(
         t.requires_grad for t in (x, top_scores, w13, w2)
     )
+    ev = stage_events if (stage_events is not None and not training) else None
+
+    def mark(name: str, end: bool) -> None:
+        if ev is not None:
+            pair = ev.setdefault(name, (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)))
+            pair[1 if end else 0].record()
+
+    scores_flat = top_scores.reshape(-1).float()
+    mark("route", False)
+    r = ops.route(selected_experts_indices, num_experts, scores_flat)
+    mark("route", True)
+    offs = r.offs
+    xb = x.to(_BF16).contiguous()
     if not training:
+        mark("permute", False)
         routed = ops.gather_rows(xb, r.sorted_indices, K, r.sorted_scores if score_before_experts else None)
-        a, _ = ops.grouped_mm_swiglu(routed, _bf16(w13), offs, swiglu_limit)
+        mark("permute", True)
+        w13b, w2b = _bf16(w13), _bf16(w2)
+        mark("gemm_w13_swiglu", False)
+        a, _ = ops.grouped_mm_swiglu(routed, w13b, offs, swiglu_limit)
+        mark("gemm_w13_swiglu", True)
         scale = None if score_before_experts else r.sorted_scores
         if K == 1:
-            out = ops.grouped_mm_unpermute(a, _bf16(w2), offs, scale, r.sorted_indices, T)
+            mark("gemm_w2_unpermute", False)
+            out = ops.grouped_mm_unpermute(a, w2b, offs, scale, r.sorted_indices, T)
+            mark("gemm_w2_unpermute", True)
         else:
-            ybuf = ops.grouped_mm_unpermute(a, _bf16(w2), offs, scale, r.sorted_indices, T * K)
+            mark("gemm_w2_unpermute", False)
+            ybuf = ops.grouped_mm_unpermute(a, w2b, offs, scale, r.sorted_indices, T * K)
+            mark("gemm_w2_unpermute", True)
+            mark("sum_topk", False)
             out = ops.sum_topk(ybuf, K)
+            mark("sum_topk", True)
         return out.to(x.dtype)
     routed = DispatchFn.apply(
         xb, scores_flat, r.sorted_indices, r.inverse, r.sorted_scores, K, score_before_experts
