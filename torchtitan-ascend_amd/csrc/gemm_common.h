@@ -21,7 +21,7 @@ __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to
 // kFwdTileRows rows for the forward GEMM, 128 for the dgrad GEMM.  The
 // workspace is sized for the smaller tiles (more of them).
 constexpr int kTileRows = 128;
-constexpr int kFwdTileRows = 256;
+constexpr int kFwdTileRows = 320;
 
 // Workspace of a token-row GEMM: int4 header {number of tiles, ...} followed
 // by the tile table.

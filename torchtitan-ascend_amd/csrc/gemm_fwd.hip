@@ -45,20 +45,29 @@
 namespace ttamd {
 namespace {
 
-constexpr int TQ = kFwdTileRows;  // 256 token rows
+constexpr int TQ = kFwdTileRows;  // 320 token rows
 constexpr int TP = 256;           // weight rows
+constexpr int WAVES = 8;          // 2 per SIMD
+constexpr int WPN = WAVES / 2;    // waves along the weight rows (2 along the token rows)
 constexpr int NJ = TQ / 64;       // 32-row token blocks per wave
+constexpr int NPB = TP / 32 / WPN;  // 32-row weight blocks per wave
 constexpr int TK = 64;            // k per stage: 128-byte rows
 constexpr int NSTAGE = 2;
-constexpr int FTHREADS = 256;
+constexpr int FTHREADS = 64 * WAVES;
 constexpr int ROW_BYTES = TK * 2;
 constexpr int P_BYTES = TP * ROW_BYTES;                // 32 KB
-constexpr int STAGE_BYTES = P_BYTES + TQ * ROW_BYTES;  // 64 KB
-constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;        // 128 KB
-constexpr int DMA_P = TP / 8 / 4;                      // 8 weight-row instructions per wave
-constexpr int DMA_Q = TQ / 8 / 4;                      // 8 token-row instructions per wave
-constexpr int DMA_PER_STAGE = DMA_P + DMA_Q;           // 16 per lane
-static_assert(TQ % 64 == 0 && TP == 256, "tile geometry");
+constexpr int STAGE_BYTES = P_BYTES + TQ * ROW_BYTES;  // 72 KB
+constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;        // 144 KB
+constexpr int DMA_P = TP / 8 / WAVES;                  // 4 weight-row instructions per wave
+constexpr int DMA_Q = TQ / 8 / WAVES;                  // 5 token-row instructions per wave
+constexpr int DMA_PER_STAGE = DMA_P + DMA_Q;           // 9 per lane
+static_assert(TQ % 64 == 0 && TP == 256 && TQ % (8 * WAVES) == 0 && NPB % 2 == 0, "tile geometry");
+// EPI_SCATTER row metadata (destination row, scale) of a tile, DMA'd with
+// the tile's first stage into one of three LDS slots (tile round % 3): the
+// slot of round r + 3 is written only after round r's epilogue.
+constexpr int META_BYTES = TQ * 8;
+constexpr int LDS_TOTAL = LDS_BYTES + 3 * META_BYTES;  // 151.5 KB
+static_assert(TQ / 64 <= WAVES, "one 64-row metadata chunk per wave");
 
 typedef __attribute__((address_space(3))) char* lds_ptr_t;
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
@@ -100,6 +109,13 @@ __device__ __forceinline__ void dma16(uint32_t voff, uint64_t sbase, uint32_t ld
                : "memory");
 }
 
+// 4 bytes per lane from sbase + voff to LDS [lds + 4 * lane].
+__device__ __forceinline__ void dma4(uint32_t voff, uint64_t sbase, uint32_t lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(uniform64(sbase)),
+               "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+
 // At most N vector-memory operations of this wave in flight, its LDS reads
 // complete, then a workgroup barrier.
 template <int N>
@@ -134,9 +150,9 @@ __device__ __forceinline__ int sload_int(const int* p) {
   return __builtin_amdgcn_readfirstlane(v);
 }
 
-// MFMA fragments of one k16 step: 4 weight blocks, NJ token blocks.
+// MFMA fragments of one k16 step: NPB weight blocks, NJ token blocks.
 struct Frag {
-  bf16x8_t a[4];
+  bf16x8_t a[NPB];
   bf16x8_t b[NJ];
 };
 
@@ -144,8 +160,8 @@ template <int EPI>
 __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wq = w >> 1;
-  const int wp = w & 1;
+  const int wq = w / WPN;
+  const int wp = w % WPN;
   const int l = threadIdx.x & 63;
   const int G = gridDim.x;
   const int b = blockIdx.x;
@@ -160,7 +176,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
 
   const uint32_t lds0 = lds_addr(smem);
   // DMA lane geometry: instruction i of wave w (per operand) writes the 8
-  // rows of row block rb = 4i + w, row 8rb + l / 8, physical chunk l % 8,
+  // rows of row block rb = WAVES*i + w, row 8rb + l / 8, physical chunk l % 8,
   // whose logical chunk is l % 8 ^ cswz(row) = l % 8 ^ ((l / 8 ^ rb) & 7).
   const int drow = l >> 3;
 
@@ -177,7 +193,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     const int qmax = ti.z - ti.y - 1;
 #pragma unroll
     for (int i = 0; i < DMA_P; ++i) {
-      const int rb = 4 * i + w;
+      const int rb = WAVES * i + w;
       const int rr = 8 * rb + drow;  // tile weight row 0..255
       const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
       int prow;
@@ -191,7 +207,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < DMA_Q; ++i) {
-      const int rb = 4 * i + w;
+      const int rb = WAVES * i + w;
       const int rr = 8 * rb + drow;  // tile token row 0..TQ-1
       const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
       d_voff[DMA_P + i] = (uint32_t)(min(rr, qmax) * a.ldq * 2 + lchunk * 16);
@@ -201,6 +217,14 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     else
       d_pbase = (uint64_t)(a.p + (int64_t)ti.x * a.p_estride + (int64_t)pt * TP * a.ldp);
     d_qbase = (uint64_t)(a.q + (int64_t)ti.y * a.ldq);
+    if constexpr (EPI == EPI_SCATTER) {
+      if (w < TQ / 64) {
+        const uint32_t q = (uint32_t)min(64 * w + l, qmax);
+        const uint32_t m = lds0 + LDS_BYTES + (uint32_t)((r % 3) * META_BYTES) + w * 256;
+        if (a.dest) dma4(q * 4, (uint64_t)(a.dest + ti.y), m);
+        if (a.row_scale) dma4(q * 4, (uint64_t)(a.row_scale + ti.y), m + TQ * 4);
+      }
+    }
     d_r = r;
   };
   auto issue = [&](int s) {
@@ -212,9 +236,9 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     const uint64_t qb = d_qbase + (uint64_t)ks * ROW_BYTES;
     const uint32_t st = lds0 + (uint32_t)((s & 1) * STAGE_BYTES) + w * 1024;
 #pragma unroll
-    for (int i = 0; i < DMA_P; ++i) dma16(d_voff[i], pb, st + i * 4096);
+    for (int i = 0; i < DMA_P; ++i) dma16(d_voff[i], pb, st + i * (WAVES * 1024));
 #pragma unroll
-    for (int i = 0; i < DMA_Q; ++i) dma16(d_voff[DMA_P + i], qb, st + P_BYTES + i * 4096);
+    for (int i = 0; i < DMA_Q; ++i) dma16(d_voff[DMA_P + i], qb, st + P_BYTES + i * (WAVES * 1024));
   };
 
   // ---- fragment geometry -------------------------------------------------------
@@ -223,15 +247,17 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   const int r32 = l & 31;
   const int half = l >> 5;
   const int fa = cswz(r32);
-  int arow[4];
+  // SWIGLU: blocks pb < NPB/2 are gate rows, pb + NPB/2 the matching up rows.
+  int arow[NPB];
 #pragma unroll
-  for (int pb = 0; pb < 4; ++pb)
-    arow[pb] = (EPI == EPI_SWIGLU) ? (pb < 2 ? 64 * wp + 32 * pb : 128 + 64 * wp + 32 * (pb - 2))
-                                   : 128 * wp + 32 * pb;
+  for (int pb = 0; pb < NPB; ++pb)
+    arow[pb] = (EPI == EPI_SWIGLU)
+                   ? (pb < NPB / 2 ? (128 / WPN) * wp + 32 * pb : 128 + (128 / WPN) * wp + 32 * (pb - NPB / 2))
+                   : (TP / WPN) * wp + 32 * pb;
   auto read_frag = [&](Frag& f, int s, int kk) {
     const char* st = smem + (s & 1) * STAGE_BYTES;
 #pragma unroll
-    for (int pb = 0; pb < 4; ++pb) {
+    for (int pb = 0; pb < NPB; ++pb) {
       const int pc = (2 * kk + half) ^ fa ^ (4 * ((arow[pb] >> 5) & 1));
       f.a[pb] = *(const bf16x8_t*)(st + (arow[pb] + r32) * ROW_BYTES + pc * 16);
     }
@@ -251,10 +277,10 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   read_frag(f0, 0, 0);
 
   int s = 0;
-  auto run_tile = [&](int row0, int row1, int pt) {
-    floatx16_t acc[4][NJ];
+  auto run_tile = [&](int r, int row0, int row1, int pt) {
+    floatx16_t acc[NPB][NJ];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NPB; ++i)
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
 #pragma unroll
@@ -263,37 +289,13 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
 #pragma unroll
-        for (int pb = 0; pb < 4; ++pb)
+        for (int pb = 0; pb < NPB; ++pb)
           acc[pb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[pb], f.b[j], acc[pb][j], 0, 0, 0);
     };
-    // Per-row epilogue operands, loaded while the tile's k loop runs.  The
-    // compiler cannot see the DMA counts, so it would wait for every memory
-    // operation before their first use; touching them right after each stage
-    // barrier (where nothing is in flight) puts that wait where it is free.
-    int dst[NJ];
-    float rsc[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int gq = row0 + NJ * 32 * wq + 32 * j + r32;
-      dst[j] = gq;
-      rsc[j] = 1.f;
-      if constexpr (EPI == EPI_SCATTER) {
-        const bool row_ok = gq < row1;
-        if (a.dest) dst[j] = row_ok ? a.dest[gq] : 0;  // clamped at use
-        if (a.row_scale) rsc[j] = row_ok ? a.row_scale[gq] : 0.f;
-      }
-    }
-
     // One stage: k16 steps 0..3, each computed from registers while the next
     // is read.  Before step 3 every wave has read all of stage s; the barrier
     // there also waits for stage s + 1 (the only stage in flight), and stage
     // s + 2 is issued into stage s's buffer.
-    auto touch_epilogue_operands = [&]() {
-      if constexpr (EPI == EPI_SCATTER) {
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) asm volatile("" ::"v"(dst[j]), "v"(rsc[j]));
-      }
-    };
     for (int ks = 0; ks + 1 < ksteps; ++ks, ++s) {
       read_frag(f1, s, 1);
       mfma(f0);
@@ -302,7 +304,6 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
       read_frag(f1, s, 3);
       mfma(f0);
       wait_vm_barrier<0>();
-      touch_epilogue_operands();
       issue(s + 2);
       read_frag(f0, s + 1, 0);
       mfma(f1);
@@ -316,7 +317,6 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     read_frag(f1, s, 3);
     mfma(f0);
     wait_vm_barrier<0>();
-    touch_epilogue_operands();
     issue(s + 2);
     mfma(f1);
     ++s;
@@ -326,25 +326,30 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     //      wave-uniform (H % 64 == 0 and N % 128 == 0 are required), row
     //      validity is per lane.  The scheduling barriers keep each block's
     //      accumulator reads next to their use (no 256-register hoist).
+    //      The lane row is re-materialised here (opaque copy) so that the
+    //      compiler does not keep per-block row offsets live across the k
+    //      loop, where every register is taken.
+    int er32 = r32;
+    asm volatile("" : "+v"(er32));
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const int gq = row0 + NJ * 32 * wq + 32 * j + r32;
+      const int gq = row0 + NJ * 32 * wq + 32 * j + er32;
       const bool row_ok = gq < row1;
       if constexpr (EPI == EPI_SWIGLU) {
         const bool clamp = (a.limit == a.limit);
         const float L = a.limit;
-        if (pt * 128 + 64 * wp < a.n_p) {
+        if (pt * 128 + (128 / WPN) * wp < a.n_p) {
 #pragma unroll
-          for (int pb = 0; pb < 2; ++pb) {
+          for (int pb = 0; pb < NPB / 2; ++pb) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-              const int col = pt * 128 + 64 * wp + 32 * pb + 8 * g + 4 * half;
+              const int col = pt * 128 + (128 / WPN) * wp + 32 * pb + 8 * g + 4 * half;
               float av[4], gv[4], uv[4];
 #pragma unroll
               for (int i = 0; i < 4; ++i) {
                 // h is materialised in bf16 by the reference; SwiGLU reads it.
                 gv[i] = round_bf16(acc[pb][j][4 * g + i]);
-                uv[i] = round_bf16(acc[pb + 2][j][4 * g + i]);
+                uv[i] = round_bf16(acc[pb + NPB / 2][j][4 * g + i]);
                 float gc = gv[i], uc = uv[i];
                 if (clamp) {
                   gc = fminf(gc, L);
@@ -367,14 +372,17 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
           }
         }
       } else {
-        const float sc = rsc[j];
-        int orow_idx = dst[j];
+        float sc = 1.f;
+        int orow_idx = gq;
         if constexpr (EPI == EPI_SCATTER) {
-          if (a.dest) orow_idx = min(max(orow_idx, 0), a.n_dest - 1);
+          const int* meta = (const int*)(smem + LDS_BYTES + (r % 3) * META_BYTES);
+          const int qrow = NJ * 32 * wq + 32 * j + er32;
+          if (a.dest) orow_idx = min(max(meta[qrow], 0), a.n_dest - 1);
+          if (a.row_scale) sc = __int_as_float(meta[TQ + qrow]);
         }
         bf16_t* orow = a.out + (int64_t)orow_idx * a.ldo;
 #pragma unroll
-        for (int pb = 0; pb < 4; ++pb) {
+        for (int pb = 0; pb < NPB; ++pb) {
           if (pt * TP + arow[pb] < a.n_p) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
@@ -397,7 +405,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     const int qt = tile / a.np_tiles;
     const int pt = tile - qt * a.np_tiles;
     const int4 ti = sload_int4(a.table + qt);
-    run_tile(ti.y, ti.z, pt);
+    run_tile(r, ti.y, ti.z, pt);
   }
   wait_vm<0>();  // DMAs past the end have landed before the workgroup exits
 }
@@ -407,12 +415,12 @@ hipError_t launch_fwd(FwdArgs a, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t err = hipFuncSetAttribute((const void*)gg_fwd_kernel<EPI>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, LDS_TOTAL);
     if (err != hipSuccess) return err;
     attr_set = true;
   }
   const int grid = (num_cus() + 7) & ~7;
-  hipLaunchKernelGGL(gg_fwd_kernel<EPI>, dim3(grid), dim3(FTHREADS), LDS_BYTES, stream, a);
+  hipLaunchKernelGGL(gg_fwd_kernel<EPI>, dim3(grid), dim3(FTHREADS), LDS_TOTAL, stream, a);
   return hipGetLastError();
 }
 
