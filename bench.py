@@ -11,7 +11,7 @@ Prints ONE JSON line (bench contract) with `roofline` for the dominant
 kernel (the w13 grouped GEMM, timed live with HIP events on the stream it
 runs on) and `cpu_baseline` (the CPU oracle on a bounded token sample).
 
-Other configs (--config c1|c3|c4) are for development runs.
+Other configs (--config c1|c3|c4|c5) are for development runs.
 """
 from __future__ import annotations
 
@@ -28,6 +28,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "MoE-layer tokens/s + grouped-GEMM TFLOP/s (% MFMA peak), Qwen3-30B-A3B shape"
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_FP8_TFLOPS = 5000.0  # MI355X dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0
 
 CONFIGS = {
@@ -39,6 +40,9 @@ CONFIGS = {
                K=1, router="sigmoid", norm=False, score_before=True, backward=True),
     "c4": dict(name="C4 DeepSeek-V3 expert shard forward (Zipf 1.2)", T=32768, D=7168, H=2048, E=32, K=1,
                router="zipf", norm=False, score_before=False, backward=False),
+    "c5": dict(name="C5 DeepSeek-V3 expert shard forward, fp8 e4m3 experts (128x128 weight scales, "
+                    "1x128 activation scales, Zipf 1.2)", T=32768, D=7168, H=2048, E=32, K=1,
+               router="zipf", norm=False, score_before=False, backward=False, fp8=True),
 }
 
 
@@ -120,8 +124,17 @@ def main():
         pair[1].record()
         return out
 
+    fp8 = cfg.get("fp8", False)
+    if fp8:
+        # weights are quantised once, as a checkpoint would be; not timed
+        w13q, s13 = ops.quantize_fp8_blocks(w13)
+        w2q, s2 = ops.quantize_fp8_blocks(w2)
+
     def step_forward(ev=None):
         scores, idx = timed_router(ev)
+        if fp8:
+            return F.moe_experts_forward_fp8(x, scores, idx, w13q, s13, w2q, s2, E, cfg["score_before"],
+                                             stage_events=ev)
         return F.moe_experts_forward(x, scores, idx, w13, w2, E, cfg["score_before"], stage_events=ev)
 
     if cfg["backward"]:
@@ -184,8 +197,14 @@ def main():
     gemm_tflops = (w13_flops + w2_flops) / (gemm_us * 1e-6) / 1e12
     w13_tflops = w13_flops / (stage_us["gemm_w13_swiglu"] * 1e-6) / 1e12
     w2_tflops = w2_flops / (stage_us["gemm_w2_unpermute"] * 1e-6) / 1e12
-    permute_bytes = T * D * 2 + M * D * 2 + 8 * M
-    permute_gbs = permute_bytes / (stage_us["permute"] * 1e-6) / 1e9
+    if fp8:
+        # gather + quantise: read x once, write e4m3 rows and their scales, indices
+        permute_bytes = T * D * 2 + M * D + M * (D // 128) * 4 + 8 * M
+        permute_gbs = permute_bytes / (stage_us["permute_quantize"] * 1e-6) / 1e9
+    else:
+        permute_bytes = T * D * 2 + M * D * 2 + 8 * M
+        permute_gbs = permute_bytes / (stage_us["permute"] * 1e-6) / 1e9
+    peak = PEAK_FP8_TFLOPS if fp8 else PEAK_BF16_TFLOPS
 
     fwd_flops = 6.0 * M * D * H
     total_flops = fwd_flops * (3 if cfg["backward"] else 1)
@@ -201,26 +220,27 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp8-e4m3 (fp32 block scales, fp32 accumulate)" if fp8 else "bf16",
         "data": "synthetic: x~N(0,1), weights~N(0,0.02), random-init router",
         "config": {"workload": cfg["name"], "tokens": T, "dim": D, "hidden": H, "experts": E, "top_k": K,
                    "router": cfg["router"], "score_before_experts": cfg["score_before"],
                    "backward": cfg["backward"]},
         "layer_tflops": round(total_flops / (ms * 1e-3) / 1e12, 1),
         "grouped_gemm_tflops": round(gemm_tflops, 1),
-        "grouped_gemm_frac_of_peak": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
+        "grouped_gemm_frac_of_peak": round(gemm_tflops / peak, 4),
         "gemm_w13_tflops": round(w13_tflops, 1),
         "gemm_w2_tflops": round(w2_tflops, 1),
         "permute_gbs": round(permute_gbs, 1),
         "permute_frac_of_hbm": round(permute_gbs / PEAK_HBM_GBS, 4),
         "stage_us": {k: round(v, 2) for k, v in stage_us.items()},
         "roofline": {
-            "kernel": "gg_fwd_kernel<EPI_SWIGLU> (grouped GEMM w13 + SwiGLU epilogue)",
+            "kernel": ("gg_fp8_kernel<EPI_SWIGLU> (fp8 grouped GEMM w13 + SwiGLU epilogue)" if fp8 else
+                       "gg_fwd_kernel<EPI_SWIGLU> (grouped GEMM w13 + SwiGLU epilogue)"),
             "bound": "mfma",
             "achieved": round(w13_tflops, 1),
-            "peak": PEAK_BF16_TFLOPS,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": round(w13_tflops / PEAK_BF16_TFLOPS, 4),
+            "frac": round(w13_tflops / peak, 4),
             "traffic": measured_traffic(args.config),
             "algorithmic_flops_per_launch": w13_flops,
             "avg_launch_us": round(stage_us["gemm_w13_swiglu"], 2),

@@ -287,6 +287,78 @@ int ttamd_grouped_mm_wgrad(const void* dy, const void* x, const int32_t* offs,
                            void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* ------------------------------------------------------------------------ *
+ * fp8 e4m3 experts with fp32 block scales.               *
+ * The reference has no fp8 path; these follow the published recipe the      *
+ * north star names: scale = absmax / 448 per block, code = e4m3fn(v /       *
+ * scale) rounded to nearest even, value = code * scale, GEMM in fp32.      *
+ * e4m3 is the OCP "fn" format (bias 7, max 448, 0x7f = NaN).  An all-zero   *
+ * block has scale 0 and codes 0.  Inputs are finite.                        *
+ * ------------------------------------------------------------------------ */
+
+/*
+ * Activations: one scale per row and 128 channels.
+ *   row j of the output is input row src_index[j] / src_div (src_index
+ *   nullable -> j), optionally multiplied by row_scale[j] in fp32 and
+ *   rounded to bf16 first (score-before-experts dispatch);
+ *   q_out uint8 [num_rows, k]; scale_t fp32 [k / 128, num_rows] (k-block
+ *   major, the layout the fp8 GEMMs read).
+ * Fuses the permute gather of ttamd_moe_gather_rows with the quantisation.
+ * k % 128 == 0, k <= 8192.
+ */
+int ttamd_quantize_fp8_rows(const void* in, const int32_t* src_index, int src_div,
+                            const float* row_scale, int64_t num_in_rows,
+                            int64_t num_rows, int64_t k, void* q_out,
+                            float* scale_t, void* stream);
+
+/*
+ * Weights: one scale per 128 x 128 block of each expert matrix.
+ * w bf16 [E, n, k] -> q_out uint8 [E, n, k], scale fp32 [E, n/128, k/128].
+ * n % 128 == 0, k % 128 == 0, k <= 8192.
+ */
+int ttamd_quantize_fp8_blocks(const void* w, int num_experts, int64_t n,
+                              int64_t k, void* q_out, float* scale,
+                              void* stream);
+
+/*
+ * fp8 grouped GEMM: out[m, n] = sum_k (xq[m,k] * sx) * (wq[e(m),n,k] * sw)
+ * with fp32 accumulation, bf16 out.  xq uint8 [M, k], sx_t fp32 [k/128, M]
+ * (from ttamd_quantize_fp8_rows), wq uint8 [E, n, k], sw fp32
+ * [E, n/128, k/128].  Replaces npu_gmm.py:31/:38's torch._grouped_mm on
+ * dequantised operands.  n % 128 == 0, k % 128 == 0.
+ */
+int ttamd_grouped_mm_fp8(const void* xq, const float* sx_t, const void* wq,
+                         const float* sw, const int32_t* offs, int64_t num_rows,
+                         int num_experts, int64_t n, int64_t k, void* out,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * fp8 version of ttamd_grouped_mm_swiglu: w13q [E, 2H, D] with scales
+ * [E, 2H/128, D/128]; same clamp, SwiGLU and bf16 outputs (a [M, H],
+ * optional h [M, 2H]).  H % 64 == 0, D % 128 == 0.
+ */
+int ttamd_grouped_mm_fp8_swiglu(const void* xq, const float* sx_t,
+                                const void* w13q, const float* s13,
+                                const int32_t* offs, int64_t num_rows,
+                                int num_experts, int64_t hidden, int64_t dim,
+                                float swiglu_limit, void* a_out, void* h_out,
+                                void* workspace, size_t workspace_bytes,
+                                void* stream);
+
+/*
+ * fp8 version of ttamd_grouped_mm_unpermute: aq uint8 [M, H] with sa_t
+ * [H/128, M], w2q [E, D, H] with scales [E, D/128, H/128]; same routing
+ * scale and scatter.  D % 128 == 0, H % 128 == 0.
+ */
+int ttamd_grouped_mm_fp8_unpermute(const void* aq, const float* sa_t,
+                                   const void* w2q, const float* s2,
+                                   const int32_t* offs, int64_t num_rows,
+                                   int num_experts, int64_t dim, int64_t hidden,
+                                   const float* row_scale, const int32_t* dest,
+                                   int64_t num_dest_rows, void* out,
+                                   void* workspace, size_t workspace_bytes,
+                                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,6 +32,12 @@ PINNED = {
     "moe_forward": "per-token brute loop of model.py:703-735 form",
     "moe_backward": "torch autograd of a torch fp32 restatement (golden); central finite differences",
     "bf16_round": "torch .to(bfloat16) on random and special values",
+    "f32_to_e4m3_bits / e4m3_bits_to_f32": "torch .to(float8_e4m3fn) on every bf16 bit pattern, ties and edge "
+                                          "values; the 256-entry decode table vs torch float8 -> float",
+    "quantize_fp8_rows / quantize_fp8_blocks": "torch float8 golden of the absmax/448 recipe; invariants: "
+                                               "|q*s - v| <= half an e4m3 step of v, max |q| == 448 per block",
+    "grouped_mm_fp8 / moe_forward_fp8": "grouped_mm (pinned above) on the dequantised operands; "
+                                        "bf16 forward within fp8 error",
 }
 
 
@@ -340,6 +346,139 @@ def moe_backward(x, top_scores, idx, w13, w2, num_experts, score_before_experts,
     else:
         np.add.at(dx, tok, d_routed)
     return {"dx": dx, "dscores": dscores.reshape(T, K), "dw13": dw13, "dw2": dw2}
+
+
+# ---------------------------------------------------------------------------
+# fp8 e4m3 with block scales (not in the reference, which
+# has no fp8 path: the published recipe is restated -- s = absmax / 448 per
+# block, q = e4m3fn(v / s), dequantised value q * s, GEMM in fp32).
+# ---------------------------------------------------------------------------
+FP8_MAX = 448.0
+FP8_BLOCK = 128
+
+
+def f32_to_e4m3_bits(a: np.ndarray) -> np.ndarray:
+    """float32 -> OCP float8 e4m3fn bits (bias 7, no infinities), round to
+    nearest even.  Magnitudes above 464 (half-way to the non-existent 480),
+    infinities and NaN give NaN (0x7f | sign), as torch.float8_e4m3fn does.
+    Computed in float64 from the decomposed value (exact), not by bit tricks."""
+    a = np.asarray(a, np.float32)
+    sign = ((a.view(np.uint32) >> 31).astype(np.uint8) << 7)
+    with np.errstate(invalid="ignore"):
+        v = np.abs(a.astype(np.float64))
+    nan = ~(v <= 464.0)  # NaN, inf and > 464
+    v = np.where(nan, 0.0, v)
+    # exponent of the result's quantum: normals 2^(e-3), subnormals 2^-9
+    with np.errstate(divide="ignore"):
+        e = np.floor(np.log2(np.where(v > 0, v, 1.0)))
+    e = np.clip(e, -6, 8)
+    quantum = np.exp2(e - 3)
+    r = np.rint(v / quantum) * quantum  # exact: v / quantum has <= 24 significant bits
+    # encode r (0 <= r <= 448)
+    with np.errstate(divide="ignore"):
+        er = np.floor(np.log2(np.where(r > 0, r, 1.0)))
+    normal = r >= 2.0 ** -6
+    exp_field = np.where(normal, er + 7, 0)
+    mant = np.where(normal, r / np.exp2(er) - 1.0, r / 2.0 ** -9) * np.where(normal, 8.0, 1.0)
+    bits = (exp_field.astype(np.int64) << 3) | np.rint(mant).astype(np.int64)
+    bits = np.where(nan, 0x7F, bits).astype(np.uint8)
+    return bits | sign
+
+
+def _e4m3_table() -> np.ndarray:
+    t = np.zeros(256, np.float32)
+    for b in range(256):
+        s = -1.0 if b & 0x80 else 1.0
+        e = (b >> 3) & 0xF
+        m = b & 7
+        if e == 0xF and m == 7:
+            t[b] = np.nan
+        elif e == 0:
+            t[b] = s * m * 2.0 ** -9
+        else:
+            t[b] = s * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+    return t
+
+
+E4M3_VALUES = _e4m3_table()
+
+
+def e4m3_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return E4M3_VALUES[np.asarray(bits, np.uint8)]
+
+
+def _block_quant(v: np.ndarray, axis_block_shape) -> tuple[np.ndarray, np.ndarray]:
+    """Quantise v (float32, already reshaped so that the block elements span
+    the axes in axis_block_shape) -> (bits, scale).  scale = absmax / 448 in
+    fp32; q = e4m3(v / scale) with the fp32 quotient; an all-zero block has
+    scale 0 and codes 0."""
+    amax = np.max(np.abs(v), axis=axis_block_shape, keepdims=True).astype(np.float32)
+    scale = (amax / np.float32(FP8_MAX)).astype(np.float32)
+    safe = np.where(scale > 0, scale, np.float32(1.0)).astype(np.float32)
+    q = (v / safe).astype(np.float32)
+    bits = np.where(scale > 0, f32_to_e4m3_bits(q), np.uint8(0)).astype(np.uint8)
+    return bits, scale
+
+
+def quantize_fp8_rows(x: np.ndarray, block: int = FP8_BLOCK) -> tuple[np.ndarray, np.ndarray]:
+    """Activations: per row, per `block` consecutive channels.
+    x [R, K] -> (bits uint8 [R, K], scale fp32 [R, K / block])."""
+    x = np.asarray(x, np.float32)
+    R, K = x.shape
+    v = x.reshape(R, K // block, block)
+    bits, scale = _block_quant(v, (2,))
+    return bits.reshape(R, K), scale.reshape(R, K // block)
+
+
+def quantize_fp8_blocks(w: np.ndarray, block: int = FP8_BLOCK) -> tuple[np.ndarray, np.ndarray]:
+    """Weights: per block x block tile of each expert matrix.
+    w [E, N, K] -> (bits uint8 [E, N, K], scale fp32 [E, N / block, K / block])."""
+    w = np.asarray(w, np.float32)
+    E, N, K = w.shape
+    v = w.reshape(E, N // block, block, K // block, block)
+    bits, scale = _block_quant(v, (2, 4))
+    return (bits.reshape(E, N, K), scale.reshape(E, N // block, K // block))
+
+
+def dequant_rows(bits: np.ndarray, scale: np.ndarray, block: int = FP8_BLOCK) -> np.ndarray:
+    R, K = bits.shape
+    return (e4m3_bits_to_f32(bits).reshape(R, K // block, block) * scale[:, :, None]).reshape(R, K)
+
+
+def dequant_blocks(bits: np.ndarray, scale: np.ndarray, block: int = FP8_BLOCK) -> np.ndarray:
+    E, N, K = bits.shape
+    v = e4m3_bits_to_f32(bits).reshape(E, N // block, block, K // block, block)
+    return (v * scale[:, :, None, :, None]).reshape(E, N, K)
+
+
+def grouped_mm_fp8(xq, sx, wq, sw, offs) -> np.ndarray:
+    """fp8 grouped GEMM: dequantise both operands (q * s) and run the fp32
+    grouped GEMM.  xq [M, K], sx [M, K/128], wq [E, N, K], sw [E, N/128, K/128]."""
+    return grouped_mm(dequant_rows(xq, sx), dequant_blocks(wq, sw), offs)
+
+
+def moe_forward_fp8(x, top_scores, idx, w13q, s13, w2q, s2, num_experts, score_before_experts,
+                    swiglu_limit=None):
+    """moe_forward with fp8 experts: the dispatched rows
+    are quantised per token and 128 channels, w13/w2 are pre-quantised with
+    128 x 128 block scales, h and a are materialised in bf16 as in the bf16
+    path, and the SwiGLU output is re-quantised per row for the w2 GEMM."""
+    T, D = x.shape
+    K = top_scores.shape[-1]
+    flat_scores = np.asarray(top_scores, np.float32).reshape(-1)
+    sidx = stable_order(idx, num_experts)
+    counts = histogram(idx, num_experts)
+    offs = np.cumsum(counts).astype(np.int64)
+    routed = np.asarray(x, np.float32)[sidx // K]
+    if score_before_experts:
+        routed = bf16_round(routed * flat_scores[sidx][:, None])
+    xq, sx = quantize_fp8_rows(routed)
+    h = bf16_round(grouped_mm_fp8(xq, sx, w13q, s13, offs))
+    a = bf16_round(swiglu(h, swiglu_limit))
+    aq, sa = quantize_fp8_rows(a)
+    y = bf16_round(grouped_mm_fp8(aq, sa, w2q, s2, offs))
+    probs = None if score_before_experts else flat_scores
+    return unpermute(y, sidx, probs, K)
 
 
 def max_rel_err(got: np.ndarray, ref: np.ndarray) -> float:

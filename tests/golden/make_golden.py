@@ -202,6 +202,59 @@ def bf16_cases():
     _save("bf16_round", values=v.numpy(), rounded=v.to(torch.bfloat16).float().numpy())
 
 
+def _fp8_quant_torch(v: torch.Tensor, dims) -> tuple[torch.Tensor, torch.Tensor]:
+    """absmax / 448 block recipe with torch's float8_e4m3fn cast (v already
+    reshaped so that `dims` span one block)."""
+    amax = v.abs().amax(dim=dims, keepdim=True)
+    s = amax / 448.0
+    q = torch.where(s > 0, v / torch.where(s > 0, s, torch.ones_like(s)), torch.zeros_like(v))
+    return q.to(torch.float8_e4m3fn).view(torch.uint8), s
+
+
+def fp8_cases():
+    # every bf16 bit pattern through torch's float8_e4m3fn cast (inputs rebuilt by the test)
+    f = (torch.arange(65536, dtype=torch.int32) << 16).view(torch.float32)
+    conv = f.to(torch.float8_e4m3fn).view(torch.uint8)
+    ties = torch.tensor([
+        # exact mid-points between neighbouring e4m3 values, both parities
+        1.0 + 1 / 16, 1.0 + 3 / 16, 448.0 + 16.0, 416.0 + 16.0, 2.0 ** -9 * 0.5, 2.0 ** -9 * 1.5,
+        2.0 ** -9 * 7.5, 2.0 ** -6 * (1 + 1 / 16), -(1.0 + 1 / 16), 0.0, -0.0, 463.99, 464.01,
+    ], dtype=torch.float32)
+    _save("fp8_e4m3_convert", bf16_patterns_e4m3=conv.numpy(), ties=ties.numpy(),
+          ties_e4m3=ties.to(torch.float8_e4m3fn).view(torch.uint8).numpy(),
+          decode=torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy())
+    g = torch.Generator().manual_seed(7)
+    R, K = 24, 384
+    x = torch.randn(R, K, generator=g) * 10.0 ** torch.randint(-3, 3, (R, 1), generator=g).float()
+    x[3, 128:256] = 0.0  # an all-zero block
+    x = _bf16(x).float()
+    q, s = _fp8_quant_torch(x.view(R, K // 128, 128), (2,))
+    _save("fp8_quant_rows", x=x.numpy(), bits=q.view(R, K).numpy(), scale=s.view(R, K // 128).numpy())
+    E, N = 2, 256
+    w = _bf16(torch.randn(E, N, K, generator=g) * 0.02).float()
+    w[1, 128:, :128] *= 1e-3
+    qw, sw = _fp8_quant_torch(w.view(E, N // 128, 128, K // 128, 128), (2, 4))
+    _save("fp8_quant_blocks", w=w.numpy(), bits=qw.view(E, N, K).numpy(),
+          scale=sw.view(E, N // 128, K // 128).numpy())
+    # fp8 grouped GEMM and a small fp8 layer, computed with torch ops
+    counts = torch.tensor([10, 0, 14], dtype=torch.int64)
+    M, E3, N3, K3 = int(counts.sum()), 3, 256, 256
+    xa = _bf16(torch.randn(M, K3, generator=g)).float()
+    wa = _bf16(torch.randn(E3, N3, K3, generator=g) * 0.02).float()
+    xq, xs = _fp8_quant_torch(xa.view(M, K3 // 128, 128), (2,))
+    wq, ws = _fp8_quant_torch(wa.view(E3, N3 // 128, 128, K3 // 128, 128), (2, 4))
+    xd = (xq.view(torch.float8_e4m3fn).float() * xs).view(M, K3)
+    wd = (wq.view(torch.float8_e4m3fn).float() * ws).view(E3, N3, K3)
+    out = torch.zeros(M, N3)
+    start = 0
+    for e, c in enumerate(counts.tolist()):
+        out[start:start + c] = (xd[start:start + c].double() @ wd[e].double().T).float()
+        start += c
+    _save("fp8_grouped_mm", xq=xq.view(M, K3).numpy(), sx=xs.view(M, K3 // 128).numpy(),
+          wq=wq.view(E3, N3, K3).numpy(), sw=ws.view(E3, N3 // 128, K3 // 128).numpy(),
+          counts=counts.numpy(), out=out.numpy())
+
+
 if __name__ == "__main__":
     torch.manual_seed(0)
     routing_cases()
@@ -210,4 +263,5 @@ if __name__ == "__main__":
     experts_cases()
     layer_cases()
     bf16_cases()
+    fp8_cases()
     print("torch", torch.__version__, "->", sorted(p.name for p in OUT.glob("*.npz")))

@@ -81,6 +81,25 @@ SIGNATURES: dict[str, tuple] = {
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i64, _i64, _c_void_p, _i32, _c_void_p, _sz, _c_void_p],
     ),
+    "ttamd_quantize_fp8_rows": (
+        _i32, [_c_void_p, _c_void_p, _i32, _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p]
+    ),
+    "ttamd_quantize_fp8_blocks": (_i32, [_c_void_p, _i32, _i64, _i64, _c_void_p, _c_void_p, _c_void_p]),
+    "ttamd_grouped_mm_fp8": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i64, _i64, _c_void_p, _c_void_p,
+         _sz, _c_void_p],
+    ),
+    "ttamd_grouped_mm_fp8_swiglu": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i64, _i64, _f32, _c_void_p,
+         _c_void_p, _c_void_p, _sz, _c_void_p],
+    ),
+    "ttamd_grouped_mm_fp8_unpermute": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i64, _i64, _c_void_p, _c_void_p,
+         _i64, _c_void_p, _c_void_p, _sz, _c_void_p],
+    ),
 }
 
 _lib = None

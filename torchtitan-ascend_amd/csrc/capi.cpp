@@ -434,4 +434,129 @@ int ttamd_grouped_mm_wgrad(const void* dy, const void* x, const int32_t* offs, i
                    fn);
 }
 
+// ---------------------------------------------------------------------------
+// fp8 e4m3 path
+// ---------------------------------------------------------------------------
+namespace {
+
+int check_fp8_k(const char* fn, const char* name, int64_t k) {
+  if (k <= 0 || k % 128 != 0 || k > 8192)
+    return fail(TTAMD_EINVAL, "%s: %s must be a positive multiple of 128 up to 8192 (got %lld)", fn, name,
+                (long long)k);
+  return TTAMD_OK;
+}
+
+int check_bytes(const char* fn, const char* name, const void* p, int64_t n) {
+  if (n > 0 && p == nullptr) return fail(TTAMD_EINVAL, "%s: %s is null", fn, name);
+  if (n > 0 && !aligned16(p)) return fail(TTAMD_EINVAL, "%s: %s must be 16-byte aligned", fn, name);
+  if (n > (int64_t(1) << 34)) return fail(TTAMD_EINVAL, "%s: %s too large", fn, name);
+  return TTAMD_OK;
+}
+
+int check_fp8_gemm(const char* fn, const void* xq, const float* sx, const void* wq, const float* sw,
+                   int64_t M, int E, int64_t n_rows, int64_t k) {
+  TRY(check_fp8_k(fn, "k", k));
+  TRY(check_bytes(fn, "xq", xq, M * k));
+  TRY(check_bytes(fn, "wq", wq, (int64_t)E * n_rows * k));
+  REQUIRE(M * k <= kI32Max, "%s: activation rows x k must stay below 2^31 bytes", fn);
+  REQUIRE(n_rows * k <= kI32Max, "%s: one expert's weights must stay below 2^31 bytes", fn);
+  if (M > 0) REQUIRE(sx != nullptr && sw != nullptr, "%s: null scale pointer", fn);
+  return TTAMD_OK;
+}
+
+}  // namespace
+
+int ttamd_quantize_fp8_rows(const void* in, const int32_t* src_index, int src_div, const float* row_scale,
+                            int64_t num_in_rows, int64_t num_rows, int64_t k, void* q_out, float* scale_t,
+                            void* stream) {
+  const char* fn = "ttamd_quantize_fp8_rows";
+  TRY(check_fp8_k(fn, "k", k));
+  REQUIRE(num_rows >= 0 && num_rows <= (1 << 28), "%s: num_rows out of range", fn);
+  REQUIRE(num_in_rows >= 0 && num_in_rows <= kI32Max, "%s: num_in_rows out of range", fn);
+  if (src_index == nullptr)
+    REQUIRE(num_in_rows >= num_rows, "%s: without src_index the input needs num_rows rows", fn);
+  else
+    REQUIRE(src_div >= 1 && num_in_rows >= 1, "%s: src_div must be >= 1 and the input non-empty", fn);
+  TRY(check_rows(fn, "in", in, num_in_rows, k));
+  TRY(check_bytes(fn, "q_out", q_out, num_rows * k));
+  if (num_rows > 0) REQUIRE(scale_t != nullptr, "%s: scale_t is null", fn);
+  if (num_rows == 0) return TTAMD_OK;
+  return check_hip(ttamd::launch_quantize_rows(in, src_index, src_div, row_scale, (int)num_in_rows,
+                                               (int)num_rows, (int)k, q_out, scale_t, (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_quantize_fp8_blocks(const void* w, int num_experts, int64_t n, int64_t k, void* q_out, float* scale,
+                              void* stream) {
+  const char* fn = "ttamd_quantize_fp8_blocks";
+  REQUIRE(num_experts >= 0 && num_experts <= 1024, "%s: num_experts out of range", fn);
+  TRY(check_dim(fn, "n", n, 128));
+  TRY(check_fp8_k(fn, "k", k));
+  const int64_t rows = (int64_t)num_experts * n;
+  TRY(check_rows(fn, "w", w, rows, k));
+  TRY(check_bytes(fn, "q_out", q_out, rows * k));
+  REQUIRE((int64_t)num_experts * (n / 128) * (k / 128) <= kI32Max, "%s: too many blocks", fn);
+  if (rows > 0) REQUIRE(scale != nullptr, "%s: scale is null", fn);
+  if (rows == 0) return TTAMD_OK;
+  return check_hip(ttamd::launch_quantize_blocks(w, num_experts, (int)n, (int)k, q_out, scale,
+                                                 (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_grouped_mm_fp8(const void* xq, const float* sx_t, const void* wq, const float* sw,
+                         const int32_t* offs, int64_t num_rows, int num_experts, int64_t n, int64_t k,
+                         void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "ttamd_grouped_mm_fp8";
+  TRY(check_gemm_common(fn, offs, num_rows, num_experts));
+  TRY(check_dim(fn, "n", n, 128));
+  TRY(check_fp8_gemm(fn, xq, sx_t, wq, sw, num_rows, num_experts, n, k));
+  TRY(check_rows(fn, "out", out, num_rows, n));
+  TRY(check_ws(fn, workspace, workspace_bytes, ttamd::gemm_workspace_bytes(num_rows, num_experts)));
+  if (num_rows == 0) return TTAMD_OK;
+  return check_hip(ttamd::launch_grouped_mm_fp8(xq, sx_t, wq, sw, offs, (int)num_rows, num_experts, (int)n,
+                                                (int)k, out, workspace, (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_grouped_mm_fp8_swiglu(const void* xq, const float* sx_t, const void* w13q, const float* s13,
+                                const int32_t* offs, int64_t num_rows, int num_experts, int64_t hidden,
+                                int64_t dim, float swiglu_limit, void* a_out, void* h_out, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  const char* fn = "ttamd_grouped_mm_fp8_swiglu";
+  TRY(check_gemm_common(fn, offs, num_rows, num_experts));
+  TRY(check_dim(fn, "hidden", hidden, 64));
+  TRY(check_fp8_gemm(fn, xq, sx_t, w13q, s13, num_rows, num_experts, 2 * hidden, dim));
+  TRY(check_rows(fn, "a_out", a_out, num_rows, hidden));
+  if (h_out) TRY(check_rows(fn, "h_out", h_out, num_rows, 2 * hidden));
+  TRY(check_ws(fn, workspace, workspace_bytes, ttamd::gemm_workspace_bytes(num_rows, num_experts)));
+  if (num_rows == 0) return TTAMD_OK;
+  return check_hip(ttamd::launch_grouped_mm_fp8_swiglu(xq, sx_t, w13q, s13, offs, (int)num_rows, num_experts,
+                                                       (int)hidden, (int)dim, swiglu_limit, a_out, h_out,
+                                                       workspace, (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_grouped_mm_fp8_unpermute(const void* aq, const float* sa_t, const void* w2q, const float* s2,
+                                   const int32_t* offs, int64_t num_rows, int num_experts, int64_t dim,
+                                   int64_t hidden, const float* row_scale, const int32_t* dest,
+                                   int64_t num_dest_rows, void* out, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  const char* fn = "ttamd_grouped_mm_fp8_unpermute";
+  TRY(check_gemm_common(fn, offs, num_rows, num_experts));
+  TRY(check_dim(fn, "dim", dim, 128));
+  TRY(check_fp8_gemm(fn, aq, sa_t, w2q, s2, num_rows, num_experts, dim, hidden));
+  if (dest == nullptr)
+    REQUIRE(num_dest_rows >= num_rows, "%s: out needs num_rows rows when dest is null", fn);
+  REQUIRE(num_dest_rows >= 0, "%s: negative num_dest_rows", fn);
+  REQUIRE(num_rows == 0 || num_dest_rows > 0, "%s: out has no rows", fn);
+  TRY(check_rows(fn, "out", out, num_dest_rows, dim));
+  TRY(check_ws(fn, workspace, workspace_bytes, ttamd::gemm_workspace_bytes(num_rows, num_experts)));
+  if (num_rows == 0) return TTAMD_OK;
+  return check_hip(ttamd::launch_grouped_mm_fp8_unpermute(aq, sa_t, w2q, s2, offs, (int)num_rows, num_experts,
+                                                          (int)dim, (int)hidden, row_scale, dest,
+                                                          (int)num_dest_rows, out, workspace,
+                                                          (hipStream_t)stream),
+                   fn);
+}
+
 }  // extern "C"

@@ -579,6 +579,72 @@ hipError_t launch_grouped_mm_unpermute(const void* act, const void* w2, const in
   return fwd(EPI_SCATTER, g, offs, E, M, ws, stream);
 }
 
+// ---- fp8 forward (gemm_fp8.hip) ----------------------------------------------
+static hipError_t fp8(int epi, Fp8Args a, const int* offs, int E, int M, void* ws,
+                      hipStream_t stream) {
+  hipError_t err = launch_tile_map(offs, E, M, kFp8TileRows, ws, stream);
+  if (err != hipSuccess) return err;
+  const TileTable tt = tile_table_in(ws);
+  a.table = tt.table;
+  a.n_qtiles = tt.count;
+  return launch_fp8_gemm(epi, a, stream);
+}
+
+static Fp8Args fp8_args(const void* xq, const float* sx, const void* wq, const float* sw, int M,
+                        int N_rows, int K) {
+  Fp8Args a = {};
+  a.q = (const uint8_t*)xq;
+  a.ldq = K;
+  a.p = (const uint8_t*)wq;
+  a.p_estride = (int64_t)N_rows * K;
+  a.ldp = K;
+  a.kred = K;
+  a.sx = sx;
+  a.ldsx = M;
+  a.sw = sw;
+  a.sw_estride = (int64_t)(N_rows / 128) * (K / 128);
+  return a;
+}
+
+hipError_t launch_grouped_mm_fp8(const void* xq, const float* sx, const void* wq, const float* sw,
+                                 const int* offs, int M, int E, int N, int K, void* out, void* ws,
+                                 hipStream_t stream) {
+  Fp8Args a = fp8_args(xq, sx, wq, sw, M, N, K);
+  a.np_tiles = N / 128;
+  a.out = (bf16_t*)out;
+  a.ldo = N;
+  return fp8(EPI_STORE, a, offs, E, M, ws, stream);
+}
+
+hipError_t launch_grouped_mm_fp8_swiglu(const void* xq, const float* sx, const void* w13q,
+                                        const float* s13, const int* offs, int M, int E, int H, int D,
+                                        float limit, void* a_out, void* h_out, void* ws,
+                                        hipStream_t stream) {
+  Fp8Args a = fp8_args(xq, sx, w13q, s13, M, 2 * H, D);
+  a.np_tiles = H / 64;
+  a.out = (bf16_t*)a_out;
+  a.ldo = H;
+  a.hidden = H;
+  a.limit = limit;
+  a.h_out = (bf16_t*)h_out;
+  a.ldh = 2 * (int64_t)H;
+  return fp8(EPI_SWIGLU, a, offs, E, M, ws, stream);
+}
+
+hipError_t launch_grouped_mm_fp8_unpermute(const void* aq, const float* sa, const void* w2q,
+                                           const float* s2, const int* offs, int M, int E, int D, int H,
+                                           const float* row_scale, const int* dest, int n_dest,
+                                           void* out, void* ws, hipStream_t stream) {
+  Fp8Args a = fp8_args(aq, sa, w2q, s2, M, D, H);
+  a.np_tiles = D / 128;
+  a.out = (bf16_t*)out;
+  a.ldo = D;
+  a.row_scale = row_scale;
+  a.dest = dest;
+  a.n_dest = n_dest;
+  return fp8(EPI_SCATTER, a, offs, E, M, ws, stream);
+}
+
 hipError_t launch_grouped_mm_dgrad(const void* dy, const void* w, const int* offs, int M, int E,
                                    int N, int K, void* dx, void* ws, hipStream_t stream) {
   // dx[m][k] = sum_n dy[m][n] w[e][n][k]: P index = k (contiguous in w), reduction = n.

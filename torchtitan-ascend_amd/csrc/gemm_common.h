@@ -83,11 +83,46 @@ struct FwdArgs {
   int n_dest;
 };
 
+// Kernel arguments of the fp8 forward GEMM (gemm_fp8.hip).  Activations and
+// weights are e4m3 bytes; strides are in bytes for them, in elements for
+// the scale and output arrays.
+struct Fp8Args {
+  const uint8_t* q;  // activations [M][kred] e4m3
+  int64_t ldq;
+  const uint8_t* p;  // weights, expert e at p + e * p_estride, rows of ldp bytes
+  int64_t p_estride;
+  int64_t ldp;
+  int kred;
+  int np_tiles;  // weight-row tiles per token tile
+  const int4* table;
+  const int* n_qtiles;
+  const float* sx;  // activation scales [kred/128][ldsx] (k-block major)
+  int64_t ldsx;
+  const float* sw;  // weight block scales, expert e at sw + e * sw_estride: [N/128][kred/128]
+  int64_t sw_estride;
+  bf16_t* out;
+  int64_t ldo;
+  // EPI_SWIGLU
+  int64_t hidden;
+  float limit;  // NaN = no clamp
+  bf16_t* h_out;
+  int64_t ldh;
+  // EPI_SCATTER
+  const float* row_scale;
+  const int* dest;
+  int n_dest;
+};
+
+// Token tiles of the fp8 GEMM have at most this many rows.
+constexpr int kFp8TileRows = 256;
+
 int num_cus();
 
 hipError_t launch_tile_map(const int* offs, int E, int M, int max_rows, void* ws,
                            hipStream_t stream);
 // Forward GEMM over a tile table of at most kFwdTileRows rows per tile.
 hipError_t launch_fwd_gemm(int epi, const FwdGemm& g, hipStream_t stream);
+// fp8 forward GEMM over a tile table of at most kFp8TileRows rows per tile.
+hipError_t launch_fp8_gemm(int epi, const Fp8Args& a, hipStream_t stream);
 
 }  // namespace ttamd

@@ -1,0 +1,354 @@
+// Persistent fp8 (e4m3) grouped GEMM with 128 x 128 block scales for the
+// expert FFN forward on MI355X (gfx950).
+//
+//   out[q, p] = sum_kb  sx[kb, q] * sw[e(q), p / 128, kb] *
+//                       sum_{k in block kb} xq[q, k] * wq[e(q), p, k]
+//
+// xq: routed activations, e4m3 [M, K], with per-row scales for every 128
+// channels stored k-block major, sx [K/128, M] (one contiguous run of rows per
+// k-block, so a tile's scales for one k-block are one 1 KB line run).
+// wq: weights e4m3 [E, N, K] with one fp32 scale per 128 x 128 block,
+// sw [E, N/128, K/128].  The scales are the absmax / 448 recipe; the
+// reference semantics are "dequantise both operands, fp32 GEMM".
+//
+// Tile: up to 256 token rows (Q) x 128 weight rows (P); k in stages of 128
+// (one scale block, one 128-byte line per row).
+//   * 4 waves, one per SIMD, 2 x 2: wave (wq, wp) owns token rows 128wq.. and
+//     64 weight rows (SWIGLU: 32 gate rows and the 32 matching up rows), i.e.
+//     2 x 4 blocks of v_mfma_scale_f32_32x32x64_f8f6f4 (unit hardware
+//     scales).  Each block's k = 128 partial sum is kept apart (2 MFMAs) and
+//     added into the fp32 accumulator times sx * sw, so the fp32 block
+//     scales are applied exactly once per block as in the dequantised form.
+//   * Three LDS stages of 50 KB: 16 KB weight rows + 32 KB token rows (DMA,
+//     global_load_lds_dwordx4, 8 rows per instruction, XOR-swizzled 16-byte
+//     chunks as in the bf16 kernel), 1 KB of token-row scales and one copy of
+//     the stage's weight-block scales per wave.  Two stages are in flight
+//     while the third is consumed.
+//   * Persistent workgroups, XCD-aware slots, flattened (tile, stage) DMA
+//     stream and the EPI_SCATTER metadata in LDS follow gemm_fwd.hip.
+#include "common.h"
+#include "dma_asm.h"
+#include "gemm_common.h"
+#include "kernels.h"
+
+namespace ttamd {
+namespace {
+
+using namespace dma;
+
+constexpr int TQ = 256;  // token rows
+constexpr int TP = 128;  // weight rows
+constexpr int TKB = 128;  // k per stage (bytes per row)
+constexpr int NSTAGE = 3;
+constexpr int FTHREADS = 256;
+constexpr int NJ = 4;   // 32-row token blocks per wave
+constexpr int NPB = 2;  // 32-row weight blocks per wave
+constexpr int P_BYTES = TP * TKB;  // 16 KB
+constexpr int Q_BYTES = TQ * TKB;  // 32 KB
+constexpr int SX_OFF = P_BYTES + Q_BYTES;
+constexpr int SW_OFF = SX_OFF + TQ * 4;
+constexpr int STAGE_BYTES = SW_OFF + 4 * 256;     // 50 KB
+constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;   // 150 KB
+constexpr int DMA_P = TP / 8 / 4;                 // 4
+constexpr int DMA_Q = TQ / 8 / 4;                 // 8
+constexpr int DMA_PER_STAGE = DMA_P + DMA_Q + 2;  // + scales of rows and weight blocks
+// EPI_SCATTER metadata slots (tile round % 4): tile r's slot is written
+// when its first stage is issued, three stages ahead, so with one-stage
+// tiles (k = 128) the writer runs three rounds ahead of the epilogue that
+// last read the slot; four slots keep them apart for every k.
+constexpr int META_BYTES = TQ * 8;
+constexpr int META_SLOTS = 4;
+constexpr int LDS_TOTAL = LDS_BYTES + META_SLOTS * META_BYTES;  // 158 KB
+static_assert(LDS_TOTAL <= 160 * 1024, "LDS");
+
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+
+// Chunk permutation of 128-byte LDS rows (as in gemm_fwd.hip).
+__device__ __forceinline__ int cswz(int r) { return (r ^ (r >> 3)) & 7; }
+
+// Fragments of one k64 step: NPB weight blocks, NJ token blocks, 32 bytes
+// (32 e4m3 values) per lane each.
+struct Frag8 {
+  i32x8_t a[NPB];
+  i32x8_t b[NJ];
+};
+
+template <int EPI>
+__global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wq = w >> 1;
+  const int wp = w & 1;
+  const int l = threadIdx.x & 63;
+  const int G = gridDim.x;
+  const int b = blockIdx.x;
+  const int slot = (b & 7) * (G >> 3) + (b >> 3);
+  const int ntiles = sload_int(a.n_qtiles) * a.np_tiles;
+  const int nmy = slot < ntiles ? (ntiles - slot + G - 1) / G : 0;
+  const int ksteps = a.kred / TKB;
+  const int total = nmy * ksteps;
+  if (total == 0) return;
+
+  const uint32_t lds0 = lds_addr(smem);
+  const int drow = l >> 3;
+
+  // ---- DMA stream -----------------------------------------------------------
+  int d_r = -1;
+  uint64_t d_pbase = 0, d_qbase = 0, d_sxbase = 0, d_swbase = 0;
+  uint32_t d_voff[DMA_P + DMA_Q];
+  uint32_t d_sxoff = 0, d_swoff = 0;
+  auto dma_tile = [&](int r) {
+    const int tile = r * G + slot;
+    const int qt = tile / a.np_tiles;
+    const int pt = tile - qt * a.np_tiles;
+    const int4 ti = sload_int4(a.table + qt);
+    const int qmax = ti.z - ti.y - 1;
+#pragma unroll
+    for (int i = 0; i < DMA_P; ++i) {
+      const int rb = 4 * i + w;
+      const int rr = 8 * rb + drow;  // tile weight row 0..127
+      const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
+      int prow;  // weight row relative to d_pbase
+      if constexpr (EPI == EPI_SWIGLU)
+        prow = (rr < 64) ? rr : (int)a.hidden + (rr - 64);
+      else
+        prow = rr;
+      d_voff[i] = (uint32_t)(prow * a.ldp + lchunk * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < DMA_Q; ++i) {
+      const int rb = 4 * i + w;
+      const int rr = 8 * rb + drow;
+      const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
+      d_voff[DMA_P + i] = (uint32_t)(min(rr, qmax) * a.ldq + lchunk * 16);
+    }
+    const int64_t prow0 = (EPI == EPI_SWIGLU) ? (int64_t)pt * 64 : (int64_t)pt * TP;
+    d_pbase = (uint64_t)(a.p + (int64_t)ti.x * a.p_estride + prow0 * a.ldp);
+    d_qbase = (uint64_t)(a.q + (int64_t)ti.y * a.ldq);
+    // token-row scales: wave w loads rows 64w + lane (clamped) of each k-block
+    d_sxbase = (uint64_t)(a.sx + ti.y);
+    d_sxoff = (uint32_t)(min(64 * w + l, qmax) * 4);
+    // weight-block scales: lane parity selects the gate / up block (SWIGLU)
+    const int64_t kb_n = a.kred / TKB;
+    int blk;
+    if constexpr (EPI == EPI_SWIGLU)
+      blk = (l & 1) ? (int)((a.hidden + (int64_t)pt * 64) / 128) : (pt * 64) / 128;
+    else
+      blk = pt;
+    d_swbase = (uint64_t)(a.sw + (int64_t)ti.x * a.sw_estride);
+    d_swoff = (uint32_t)(blk * kb_n * 4);
+    if constexpr (EPI == EPI_SCATTER) {
+      const uint32_t q = (uint32_t)min(64 * w + l, qmax);
+      const uint32_t m = lds0 + LDS_BYTES + (uint32_t)((r % META_SLOTS) * META_BYTES) + w * 256;
+      if (a.dest) dma4(q * 4, (uint64_t)(a.dest + ti.y), m);
+      if (a.row_scale) dma4(q * 4, (uint64_t)(a.row_scale + ti.y), m + TQ * 4);
+    }
+    d_r = r;
+  };
+  auto issue = [&](int s) {
+    const int sc = min(s, total - 1);  // past the end: re-load the last stage
+    const int r = sc / ksteps;
+    const int ks = sc - r * ksteps;
+    if (r != d_r) dma_tile(r);
+    const uint64_t pb = d_pbase + (uint64_t)ks * TKB;
+    const uint64_t qb = d_qbase + (uint64_t)ks * TKB;
+    const uint32_t st = lds0 + (uint32_t)((s % NSTAGE) * STAGE_BYTES);
+#pragma unroll
+    for (int i = 0; i < DMA_P; ++i) dma16(d_voff[i], pb, st + w * 1024 + i * 4096);
+#pragma unroll
+    for (int i = 0; i < DMA_Q; ++i) dma16(d_voff[DMA_P + i], qb, st + P_BYTES + w * 1024 + i * 4096);
+    dma4(d_sxoff, d_sxbase + (uint64_t)ks * a.ldsx * 4, st + SX_OFF + w * 256);
+    dma4(d_swoff, d_swbase + (uint64_t)ks * 4, st + SW_OFF + w * 256);
+  };
+
+  // ---- fragment geometry -------------------------------------------------------
+  const int r32 = l & 31;
+  const int half = l >> 5;
+  const int fa = cswz(r32);
+  int arow[NPB];
+#pragma unroll
+  for (int pb = 0; pb < NPB; ++pb)
+    arow[pb] = (EPI == EPI_SWIGLU) ? 32 * wp + 64 * pb : 64 * wp + 32 * pb;
+  // k64 step `sub` of a stage: lane (r32, half) takes bytes 64sub + 32half ..
+  // + 31 of its row, logical chunks c0 = 4sub + 2half and c0 + 1.
+  auto read_frag = [&](Frag8& f, int s, int sub) {
+    const char* st = smem + (s % NSTAGE) * STAGE_BYTES;
+    const int c0 = 4 * sub + 2 * half;
+#pragma unroll
+    for (int pb = 0; pb < NPB; ++pb) {
+      const int m = arow[pb] >> 5;
+      const int x = fa ^ (4 * (m & 1));
+      const char* row = st + (arow[pb] + r32) * TKB;
+      const i32x4_t lo = *(const i32x4_t*)(row + ((c0 ^ x) * 16));
+      const i32x4_t hi = *(const i32x4_t*)(row + (((c0 + 1) ^ x) * 16));
+      f.a[pb] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int m = 4 * wq + j;
+      const int x = fa ^ (4 * (m & 1));
+      const char* row = st + P_BYTES + (32 * m + r32) * TKB;
+      const i32x4_t lo = *(const i32x4_t*)(row + ((c0 ^ x) * 16));
+      const i32x4_t hi = *(const i32x4_t*)(row + (((c0 + 1) ^ x) * 16));
+      f.b[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+  };
+  float sxv[NJ], swv[NPB];
+  auto read_scales = [&](int s) {
+    const char* st = smem + (s % NSTAGE) * STAGE_BYTES;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) sxv[j] = *(const float*)(st + SX_OFF + (128 * wq + 32 * j + r32) * 4);
+#pragma unroll
+    for (int pb = 0; pb < NPB; ++pb) {
+      const int lane = (EPI == EPI_SWIGLU) ? pb : 0;
+      swv[pb] = *(const float*)(st + SW_OFF + w * 256 + lane * 4);
+    }
+  };
+
+  // ---- prologue: stages 0..2 in flight, stage 0 read --------------------------
+  issue(0);
+  issue(1);
+  issue(2);
+  wait_vm_barrier<2 * DMA_PER_STAGE>();
+  Frag8 f0, f1;
+  read_frag(f0, 0, 0);
+  read_frag(f1, 0, 1);
+  read_scales(0);
+
+  int s = 0;
+  for (int r = 0; r < nmy; ++r) {
+    const int tile = r * G + slot;
+    const int qt = tile / a.np_tiles;
+    const int pt = tile - qt * a.np_tiles;
+    const int4 ti = sload_int4(a.table + qt);
+    const int row0 = ti.y, row1 = ti.z;
+
+    floatx16_t acc[NPB][NJ];
+#pragma unroll
+    for (int i = 0; i < NPB; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+    for (int ks = 0; ks < ksteps; ++ks, ++s) {
+      // k = 128 partial sums of this stage, one per block
+      floatx16_t part[NPB][NJ];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int pb = 0; pb < NPB; ++pb) {
+          floatx16_t z = {};
+          z = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f0.a[pb], f0.b[j], z, 0, 0, 0, 127, 0, 127);
+          part[pb][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f1.a[pb], f1.b[j], z, 0, 0, 0, 127,
+                                                                         0, 127);
+        }
+      float sc[NPB][NJ];
+#pragma unroll
+      for (int pb = 0; pb < NPB; ++pb)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) sc[pb][j] = swv[pb] * sxv[j];
+      // Stage s + 1 has landed once only stage s + 2 may be in flight; every
+      // wave has read stage s (fragments and scales are in registers), so
+      // its buffer takes stage s + 3.
+      wait_vm_barrier<DMA_PER_STAGE>();
+      issue(s + NSTAGE);
+      read_frag(f0, s + 1, 0);
+      read_frag(f1, s + 1, 1);
+      read_scales(s + 1);
+#pragma unroll
+      for (int pb = 0; pb < NPB; ++pb)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[pb][j][v] += part[pb][j][v] * sc[pb][j];
+    }
+
+    // ---- epilogue: acc[pb][j][4g + i] is (token row 128wq + 32j + r32,
+    //      weight row arow[pb] + 8g + 4 * half + i).
+    int er32 = r32;
+    asm volatile("" : "+v"(er32));
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int gq = row0 + 128 * wq + 32 * j + er32;
+      const bool row_ok = gq < row1;
+      if constexpr (EPI == EPI_SWIGLU) {
+        const bool clamp = (a.limit == a.limit);
+        const float L = a.limit;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = pt * 64 + 32 * wp + 8 * g + 4 * half;
+          float av[4], gv[4], uv[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            gv[i] = round_bf16(acc[0][j][4 * g + i]);
+            uv[i] = round_bf16(acc[1][j][4 * g + i]);
+            float gc = gv[i], uc = uv[i];
+            if (clamp) {
+              gc = fminf(gc, L);
+              uc = fminf(fmaxf(uc, -L), L);
+            }
+            av[i] = silu_f(gc) * uc;
+          }
+          if (row_ok) {
+            bf16_t* orow = a.out + (int64_t)gq * a.ldo + col;
+            *(uint2*)orow = make_uint2(pack_bf16x2(av[0], av[1]), pack_bf16x2(av[2], av[3]));
+            if (a.h_out) {
+              bf16_t* hrow = a.h_out + (int64_t)gq * a.ldh + col;
+              *(uint2*)hrow = make_uint2(pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3]));
+              *(uint2*)(hrow + a.hidden) = make_uint2(pack_bf16x2(uv[0], uv[1]), pack_bf16x2(uv[2], uv[3]));
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        float scl = 1.f;
+        int orow_idx = gq;
+        if constexpr (EPI == EPI_SCATTER) {
+          const int* meta = (const int*)(smem + LDS_BYTES + (r % META_SLOTS) * META_BYTES);
+          const int qrow = 128 * wq + 32 * j + er32;
+          if (a.dest) orow_idx = min(max(meta[qrow], 0), a.n_dest - 1);
+          if (a.row_scale) scl = __int_as_float(meta[TQ + qrow]);
+        }
+        bf16_t* orow = a.out + (int64_t)orow_idx * a.ldo;
+#pragma unroll
+        for (int pb = 0; pb < NPB; ++pb) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int col = pt * TP + arow[pb] + 8 * g + 4 * half;
+            const floatx16_t& v = acc[pb][j];
+            const uint2 val = make_uint2(pack_bf16x2(v[4 * g] * scl, v[4 * g + 1] * scl),
+                                         pack_bf16x2(v[4 * g + 2] * scl, v[4 * g + 3] * scl));
+            if (row_ok) *(uint2*)(orow + col) = val;
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+  }
+  wait_vm<0>();  // DMAs past the end have landed before the workgroup exits
+}
+
+template <int EPI>
+hipError_t launch_fp8(const Fp8Args& a, hipStream_t stream) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t err = hipFuncSetAttribute((const void*)gg_fp8_kernel<EPI>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, LDS_TOTAL);
+    if (err != hipSuccess) return err;
+    attr_set = true;
+  }
+  const int grid = (num_cus() + 7) & ~7;
+  hipLaunchKernelGGL(gg_fp8_kernel<EPI>, dim3(grid), dim3(FTHREADS), LDS_TOTAL, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_fp8_gemm(int epi, const Fp8Args& a, hipStream_t stream) {
+  if (epi == EPI_SWIGLU) return launch_fp8<EPI_SWIGLU>(a, stream);
+  if (epi == EPI_SCATTER) return launch_fp8<EPI_SCATTER>(a, stream);
+  return launch_fp8<EPI_STORE>(a, stream);
+}
+
+}  // namespace ttamd

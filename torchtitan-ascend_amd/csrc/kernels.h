@@ -49,4 +49,21 @@ hipError_t launch_grouped_mm_dgrad_swiglu(const void* dy, const void* w2, const 
 hipError_t launch_grouped_mm_wgrad(const void* dy, const void* x, const int* offs, int M, int E,
                                    int N, int K, void* dw, bool fp32, hipStream_t stream);
 
+// fp8 e4m3 path (quant.hip, gemm_fp8.hip via gemm.hip)
+hipError_t launch_quantize_rows(const void* in, const int* src_index, int src_div, const float* row_mul,
+                                int n_in, int R, int K, void* q_out, float* scale_t, hipStream_t stream);
+hipError_t launch_quantize_blocks(const void* w, int E, int N, int K, void* q_out, float* scale,
+                                  hipStream_t stream);
+hipError_t launch_grouped_mm_fp8(const void* xq, const float* sx, const void* wq, const float* sw,
+                                 const int* offs, int M, int E, int N, int K, void* out, void* ws,
+                                 hipStream_t stream);
+hipError_t launch_grouped_mm_fp8_swiglu(const void* xq, const float* sx, const void* w13q,
+                                        const float* s13, const int* offs, int M, int E, int H, int D,
+                                        float limit, void* a_out, void* h_out, void* ws,
+                                        hipStream_t stream);
+hipError_t launch_grouped_mm_fp8_unpermute(const void* aq, const float* sa, const void* w2q,
+                                           const float* s2, const int* offs, int M, int E, int D, int H,
+                                           const float* row_scale, const int* dest, int n_dest,
+                                           void* out, void* ws, hipStream_t stream);
+
 }  // namespace ttamd

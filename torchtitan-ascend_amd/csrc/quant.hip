@@ -1,0 +1,159 @@
+// fp8 e4m3 quantisation with fp32 block scales (absmax / 448) on MI355X.
+//
+//   rows:   activations [R, K], one scale per row and 128 channels, written
+//           k-block major (scale_t[K/128][R]) for the fp8 GEMM's DMA; the
+//           rows can be gathered on the way (routed row j reads input row
+//           src_index[j] / src_div), which fuses the MoE permute.
+//   blocks: weights [E, N, K], one scale per 128 x 128 block ([E][N/128][K/128]).
+//
+// e4m3 here is the OCP "fn" variant (bias 7, largest finite 448, no
+// infinities, code 0x7f = NaN), the format the gfx950 fp8 MFMA reads with
+// cbsz/blgp = 0.  The conversion rounds to nearest even and is done with
+// integer operations on the float32 bits, so it does not depend on the
+// hardware conversion instructions' saturation mode.  |v| above 464 (half
+// way to 480) gives NaN, which the absmax / 448 recipe never produces.
+#include "common.h"
+#include "kernels.h"
+
+namespace ttamd {
+
+__device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
+  uint32_t u = __float_as_uint(v);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  u &= 0x7fffffffu;
+  if (u > 0x43e80000u) return sign | 0x7fu;  // > 464, inf, NaN
+  if (u < 0x3c800000u) {                     // below 2^-6: multiples of 2^-9
+    const float t = __uint_as_float(u) * 512.0f;  // exact
+    return sign | (uint32_t)__builtin_rintf(t);   // 0..8 (8 = smallest normal 0x08)
+  }
+  // keep 3 mantissa bits, round to nearest even (a carry bumps the exponent)
+  const uint32_t r = u + 0x7ffffu + ((u >> 20) & 1u);
+  const uint32_t e = (r >> 23) - 127u + 7u;
+  return sign | (e << 3) | ((r >> 20) & 7u);
+}
+
+// ---------------------------------------------------------------------------
+// Rows: a workgroup of 4 waves quantises 16 rows (4 per wave).  A wave walks
+// its row 512 channels at a time: lane l holds 8 consecutive channels, 16
+// lanes form one 128-channel block.  Scales go through LDS so that each
+// k-block's 16 row scales leave as one 64-byte store.
+// ---------------------------------------------------------------------------
+constexpr int kQRows = 16;
+constexpr int kMaxKBlocks = 64;  // K <= 8192
+
+__global__ __launch_bounds__(256) void quantize_rows_kernel(const uint4* __restrict__ in,
+                                                            const int* __restrict__ src_index,
+                                                            int src_div, const float* __restrict__ row_mul,
+                                                            int n_in, int R, int K,
+                                                            uint2* __restrict__ q_out,
+                                                            float* __restrict__ scale_t) {
+  __shared__ float sc[kMaxKBlocks][kQRows];
+  const int w = threadIdx.x >> 6;
+  const int l = threadIdx.x & 63;
+  const int row_base = blockIdx.x * kQRows;
+  const int kv = K / 8;  // 16-byte vectors per row
+  const int nkb = K / 128;
+  for (int rr = w; rr < kQRows; rr += 4) {
+    const int row = row_base + rr;
+    if (row >= R) break;
+    int src = row;
+    if (src_index) src = min(max(src_index[row] / src_div, 0), n_in - 1);
+    const float mul = row_mul ? row_mul[row] : 1.f;
+    const uint4* irow = in + (int64_t)src * kv;
+    uint2* orow = q_out + (int64_t)row * kv;
+    for (int c = l; c < ((kv + 63) & ~63); c += 64) {
+      const bool ok = c < kv;
+      float f[8];
+      if (ok) {
+        unpack8(irow[c], f);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f[i] = 0.f;
+      }
+      if (row_mul) {
+        // the dispatched row is materialised in bf16 after the score multiply
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f[i] = bf16_to_f32(f32_to_bf16(f[i] * mul));
+      }
+      float m = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(f[i]));
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+      const float s = m / 448.0f;
+      uint32_t b[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) b[i] = (s > 0.f) ? f32_to_e4m3(f[i] / s) : 0u;
+      if (ok) {
+        orow[c] = make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24),
+                             b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
+        if ((l & 15) == 0) sc[c >> 4][rr] = s;
+      }
+    }
+  }
+  __syncthreads();
+  // scale_t[kb][row_base .. row_base + 15]
+  for (int i = threadIdx.x; i < nkb * kQRows; i += 256) {
+    const int kb = i / kQRows, rr = i % kQRows;
+    if (row_base + rr < R) scale_t[(int64_t)kb * R + row_base + rr] = sc[kb][rr];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Blocks: one workgroup per 128 x 128 block; thread t covers row t / 2,
+// channels 64 (t & 1) .. + 63.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quantize_blocks_kernel(const uint4* __restrict__ w, int N, int K,
+                                                              uint2* __restrict__ q_out,
+                                                              float* __restrict__ scale) {
+  __shared__ float red[4];
+  const int nb = N / 128, kb = K / 128;
+  const int blk = blockIdx.x;
+  const int e = blk / (nb * kb);
+  const int rem = blk - e * nb * kb;
+  const int bn = rem / kb, bk = rem - bn * kb;
+  const int t = threadIdx.x;
+  const int64_t row = (int64_t)e * N + bn * 128 + (t >> 1);
+  const int64_t v0 = row * (K / 8) + bk * 16 + (t & 1) * 8;  // first 16-byte vector
+  float f[64];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) unpack8(w[v0 + i], f + 8 * i);
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) m = fmaxf(m, fabsf(f[i]));
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((t & 63) == 0) red[t >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = m / 448.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t b[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) b[j] = (s > 0.f) ? f32_to_e4m3(f[8 * i + j] / s) : 0u;
+    q_out[v0 + i] = make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24),
+                               b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
+  }
+  if (t == 0) scale[blk] = s;
+}
+
+hipError_t launch_quantize_rows(const void* in, const int* src_index, int src_div, const float* row_mul,
+                                int n_in, int R, int K, void* q_out, float* scale_t, hipStream_t stream) {
+  if (R == 0) return hipSuccess;
+  const int grid = (R + kQRows - 1) / kQRows;
+  hipLaunchKernelGGL(quantize_rows_kernel, dim3(grid), dim3(256), 0, stream, (const uint4*)in, src_index,
+                     src_div, row_mul, n_in, R, K, (uint2*)q_out, scale_t);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_blocks(const void* w, int E, int N, int K, void* q_out, float* scale,
+                                  hipStream_t stream) {
+  const int64_t nblk = (int64_t)E * (N / 128) * (K / 128);
+  if (nblk == 0) return hipSuccess;
+  hipLaunchKernelGGL(quantize_blocks_kernel, dim3((unsigned)nblk), dim3(256), 0, stream, (const uint4*)w, N,
+                     K, (uint2*)q_out, scale);
+  return hipGetLastError();
+}
+
+}  // namespace ttamd

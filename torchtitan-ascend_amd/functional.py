@@ -217,3 +217,57 @@ def moe_experts_forward(
     y = ExpertsFn.apply(routed, w13, w2, offs, swiglu_limit)
     out = CombineFn.apply(y, scores_flat, r.sorted_indices, r.inverse, K, not score_before_experts)
     return out.to(x.dtype)
+
+
+def moe_experts_forward_fp8(
+    x: torch.Tensor,
+    top_scores: torch.Tensor,
+    selected_experts_indices: torch.Tensor,
+    w13q: torch.Tensor,
+    s13: torch.Tensor,
+    w2q: torch.Tensor,
+    s2: torch.Tensor,
+    num_experts: int,
+    score_before_experts: bool,
+    swiglu_limit: float | None = None,
+    stage_events: dict | None = None,
+) -> torch.Tensor:
+    """Inference forward with fp8 e4m3 experts (weights pre-quantised with
+    ops.quantize_fp8_blocks): route -> gather + per-token quantise -> fp8
+    w13 + SwiGLU -> per-token re-quantise of a -> fp8 w2 + scale + scatter
+    -> K-way sum.  x [T, D] bf16 -> [T, D]."""
+    T, D = x.shape
+    K = top_scores.shape[-1]
+    ev = stage_events
+
+    def mark(name: str, end: bool) -> None:
+        if ev is not None:
+            pair = ev.setdefault(name, (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)))
+            pair[1 if end else 0].record()
+
+    scores_flat = top_scores.reshape(-1).float()
+    mark("route", False)
+    r = ops.route(selected_experts_indices, num_experts, scores_flat)
+    mark("route", True)
+    xb = x.to(_BF16).contiguous()
+    mark("permute_quantize", False)
+    xq, sx = ops.quantize_fp8_rows(xb, r.sorted_indices, K, r.sorted_scores if score_before_experts else None)
+    mark("permute_quantize", True)
+    mark("gemm_w13_swiglu", False)
+    a, _ = ops.grouped_mm_fp8_swiglu(xq, sx, w13q, s13, r.offs, swiglu_limit)
+    mark("gemm_w13_swiglu", True)
+    mark("quantize_a", False)
+    aq, sa = ops.quantize_fp8_rows(a)
+    mark("quantize_a", True)
+    scale = None if score_before_experts else r.sorted_scores
+    mark("gemm_w2_unpermute", False)
+    if K == 1:
+        out = ops.grouped_mm_fp8_unpermute(aq, sa, w2q, s2, r.offs, scale, r.sorted_indices, T)
+        mark("gemm_w2_unpermute", True)
+    else:
+        ybuf = ops.grouped_mm_fp8_unpermute(aq, sa, w2q, s2, r.offs, scale, r.sorted_indices, T * K)
+        mark("gemm_w2_unpermute", True)
+        mark("sum_topk", False)
+        out = ops.sum_topk(ybuf, K)
+        mark("sum_topk", True)
+    return out.to(x.dtype)

@@ -470,3 +470,120 @@ def grouped_mm_wgrad(
         int(out_dtype == torch.float32), None, 0, _stream(dev),
     )
     return dw
+
+
+# ---------------------------------------------------------------------------
+# fp8 e4m3 experts (block scales, absmax / 448)
+# ---------------------------------------------------------------------------
+_U8 = torch.uint8
+
+
+def quantize_fp8_rows(
+    x: torch.Tensor,
+    src_index: torch.Tensor | None = None,
+    src_div: int = 1,
+    row_scale: torch.Tensor | None = None,
+    num_rows: int | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row, per-128-channel e4m3 quantisation, optionally of gathered rows
+    (row j = x[src_index[j] // src_div], times row_scale[j] rounded to bf16).
+    Returns (q uint8 [R, K], scale_t fp32 [K / 128, R])."""
+    dev = _gpu("x", x)
+    x = _want("x", x, _BF16)
+    n_in, K = x.shape
+    if src_index is not None:
+        src_index = _want("src_index", src_index, torch.int32)
+        R = src_index.numel() if num_rows is None else int(num_rows)
+    else:
+        R = n_in if num_rows is None else int(num_rows)
+    if row_scale is not None:
+        row_scale = _want("row_scale", row_scale, torch.float32)
+    q = torch.empty(R, K, dtype=_U8, device=dev)
+    s = torch.empty(K // 128 if K % 128 == 0 else 0, R, dtype=torch.float32, device=dev)
+    _lib.call(
+        "ttamd_quantize_fp8_rows", _p(x), _p(src_index), int(src_div), _p(row_scale), n_in, R, K, _p(q), _p(s),
+        _stream(dev),
+    )
+    return q, s
+
+
+def quantize_fp8_blocks(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """128 x 128 block e4m3 quantisation of expert weights w [E, N, K].
+    Returns (q uint8 [E, N, K], scale fp32 [E, N / 128, K / 128])."""
+    dev = _gpu("w", w)
+    w = _want("w", w, _BF16)
+    E, N, K = w.shape
+    q = torch.empty(E, N, K, dtype=_U8, device=dev)
+    s = torch.empty(E, N // 128, K // 128, dtype=torch.float32, device=dev)
+    _lib.call("ttamd_quantize_fp8_blocks", _p(w), E, N, K, _p(q), _p(s), _stream(dev))
+    return q, s
+
+
+def _fp8_operands(xq, sx_t, wq, sw, dev):
+    xq = _want("xq", xq, _U8)
+    sx_t = _want("sx_t", sx_t, torch.float32)
+    wq = _want("wq", wq, _U8)
+    sw = _want("sw", sw, torch.float32)
+    M, K = xq.shape
+    E, N, K2 = wq.shape
+    if K2 != K:
+        raise ValueError(f"xq has K={K}, wq has K={K2}")
+    if sx_t.shape != (K // 128, M) or sw.shape != (E, N // 128, K // 128):
+        raise ValueError("scale shapes do not match the operands")
+    return xq, sx_t, wq, sw, M, K, E, N
+
+
+def grouped_mm_fp8(xq: torch.Tensor, sx_t: torch.Tensor, wq: torch.Tensor, sw: torch.Tensor,
+                   offs: torch.Tensor) -> torch.Tensor:
+    """fp8 grouped GEMM on dequantised operands, bf16 out [M, N]."""
+    dev = _gpu("xq", xq)
+    xq, sx_t, wq, sw, M, K, E, N = _fp8_operands(xq, sx_t, wq, sw, dev)
+    offs = _offs(offs, dev)
+    out = torch.empty(M, N, dtype=_BF16, device=dev)
+    ws = _gemm_ws(M, E, dev)
+    _lib.call(
+        "ttamd_grouped_mm_fp8", _p(xq), _p(sx_t), _p(wq), _p(sw), _p(offs), M, E, N, K, _p(out), _p(ws),
+        ws.numel(), _stream(dev),
+    )
+    return out
+
+
+def grouped_mm_fp8_swiglu(
+    xq: torch.Tensor, sx_t: torch.Tensor, w13q: torch.Tensor, s13: torch.Tensor, offs: torch.Tensor,
+    swiglu_limit: float | None = None, save_h: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """fp8 w13 GEMM + clamp + SwiGLU; returns (a [M, H] bf16, h [M, 2H] bf16 or None)."""
+    dev = _gpu("xq", xq)
+    xq, sx_t, w13q, s13, M, D, E, H2 = _fp8_operands(xq, sx_t, w13q, s13, dev)
+    offs = _offs(offs, dev)
+    H = H2 // 2
+    a = torch.empty(M, H, dtype=_BF16, device=dev)
+    h = torch.empty(M, 2 * H, dtype=_BF16, device=dev) if save_h else None
+    ws = _gemm_ws(M, E, dev)
+    _lib.call(
+        "ttamd_grouped_mm_fp8_swiglu", _p(xq), _p(sx_t), _p(w13q), _p(s13), _p(offs), M, E, H, D,
+        _limit(swiglu_limit), _p(a), _p(h), _p(ws), ws.numel(), _stream(dev),
+    )
+    return a, h
+
+
+def grouped_mm_fp8_unpermute(
+    aq: torch.Tensor, sa_t: torch.Tensor, w2q: torch.Tensor, s2: torch.Tensor, offs: torch.Tensor,
+    row_scale: torch.Tensor | None = None, dest: torch.Tensor | None = None, num_dest_rows: int | None = None,
+) -> torch.Tensor:
+    """fp8 w2 GEMM + routing scale + scatter: out[dest[j]] = row_scale[j] * y[j]."""
+    dev = _gpu("aq", aq)
+    aq, sa_t, w2q, s2, M, H, E, D = _fp8_operands(aq, sa_t, w2q, s2, dev)
+    offs = _offs(offs, dev)
+    if row_scale is not None:
+        row_scale = _want("row_scale", row_scale, torch.float32)
+    if dest is not None:
+        dest = _want("dest", dest, torch.int32)
+    nd = M if num_dest_rows is None else int(num_dest_rows)
+    out = torch.empty(nd, D, dtype=_BF16, device=dev)
+    ws = _gemm_ws(M, E, dev)
+    _lib.call(
+        "ttamd_grouped_mm_fp8_unpermute", _p(aq), _p(sa_t), _p(w2q), _p(s2), _p(offs), M, E, D, H, _p(row_scale),
+        _p(dest), nd, _p(out), _p(ws), ws.numel(), _stream(dev),
+    )
+    return out
