@@ -200,10 +200,13 @@ def main():
     if fp8:
         # gather + quantise: read x once, write e4m3 rows and their scales, indices
         permute_bytes = T * D * 2 + M * D + M * (D // 128) * 4 + 8 * M
-        permute_gbs = permute_bytes / (stage_us["permute_quantize"] * 1e-6) / 1e9
+        permute_us = stage_us["permute_quantize"]
     else:
+        # The inference step fuses the gather into the w13 GEMM; the standalone
+        # permute kernel (dispatcher API, training path) is timed on its own.
         permute_bytes = T * D * 2 + M * D * 2 + 8 * M
-        permute_gbs = permute_bytes / (stage_us["permute"] * 1e-6) / 1e9
+        permute_us = stage_us.get("permute") or time_standalone_permute(ops, router, x, E, K, cfg)
+    permute_gbs = permute_bytes / (permute_us * 1e-6) / 1e9
     peak = PEAK_FP8_TFLOPS if fp8 else PEAK_BF16_TFLOPS
 
     fwd_flops = 6.0 * M * D * H
@@ -230,6 +233,7 @@ def main():
         "grouped_gemm_frac_of_peak": round(gemm_tflops / peak, 4),
         "gemm_w13_tflops": round(w13_tflops, 1),
         "gemm_w2_tflops": round(w2_tflops, 1),
+        "permute_us": round(permute_us, 2),
         "permute_gbs": round(permute_gbs, 1),
         "permute_frac_of_hbm": round(permute_gbs / PEAK_HBM_GBS, 4),
         "stage_us": {k: round(v, 2) for k, v in stage_us.items()},
@@ -250,6 +254,26 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, cfg, x, w13, w2, router)
     print(json.dumps(result), flush=True)
+
+
+def time_standalone_permute(ops, router, x, E, K, cfg, reps=20):
+    """Average duration (us) of the permute gather kernel (ttamd_moe_gather_rows)
+    on this workload's routing, on the current stream."""
+    import torch
+
+    with torch.no_grad():
+        scores, idx = router()
+        r = ops.route(idx, E, scores.reshape(-1).float())
+        scale = r.sorted_scores if cfg["score_before"] else None
+        ops.gather_rows(x, r.sorted_indices, K, scale)
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s0.record()
+        for _ in range(reps):
+            ops.gather_rows(x, r.sorted_indices, K, scale)
+        s1.record()
+        torch.cuda.synchronize()
+    return s0.elapsed_time(s1) * 1000.0 / reps
 
 
 def measured_traffic(config):

@@ -225,6 +225,25 @@ int ttamd_grouped_mm_swiglu(const void* x, const void* w13,
                             void* stream);
 
 /*
+ * ttamd_grouped_mm_swiglu with the permute gather fused into its loads:
+ * routed row j is tokens[src_index[j] / src_div] (src_index =
+ * sorted_indices of ttamd_moe_route, src_div = topk), so the routed
+ * [M, D] copy is never written.  Replaces the gather of
+ * npu_moe_token_permute (npu_permute.py:74-76; upstream dispatch's
+ * index_select, reached from npu_gmm.py:106-108) plus npu_gmm.py:29-37 on
+ * the inference path (score applied after the experts).  tokens bf16
+ * [num_tokens, D] (< 4 GiB); H % 64 == 0, D % 64 == 0, D >= 128.
+ */
+int ttamd_grouped_mm_swiglu_gather(const void* tokens, int64_t num_tokens,
+                                   const int32_t* src_index, int src_div,
+                                   const void* w13, const int32_t* offs,
+                                   int64_t num_rows, int num_experts,
+                                   int64_t hidden, int64_t dim,
+                                   float swiglu_limit, void* a_out,
+                                   void* h_out, void* workspace,
+                                   size_t workspace_bytes, void* stream);
+
+/*
  * Fused expert down-projection + routing-weight scale + un-permute:
  *   y[j] = a[j] @ w2[e(j)]^T  (w2 [E, D, H]),  fp32
  *   v    = row_scale ? row_scale[j] * y[j] : y[j]

@@ -92,6 +92,26 @@ def test_grouped_mm_swiglu(ops, M, E, D, H, kind, limit):
     assert O.max_rel_err(to_np(a), O.swiglu(to_np(h), limit)) < 1e-2
 
 
+@pytest.mark.parametrize("T,K,E,D,H,kind", [(500, 2, 8, 256, 128, "random"), (1024, 4, 16, 512, 192, "zipf"),
+                                            (3000, 1, 4, 2048, 768, "random"), (64, 8, 32, 128, 64, "zipf")])
+def test_grouped_mm_swiglu_gather(ops, T, K, E, D, H, kind):
+    """The permute gather fused into the w13 loads: routed row j is
+    x[sorted_indices[j] // K]; compared with the gathered-then-GEMM oracle."""
+    rng = np.random.default_rng(T + K + D)
+    M = T * K
+    counts = _counts(kind, M, E, rng)
+    labels = rng.permutation(np.repeat(np.arange(E), counts))
+    sidx = O.stable_order(labels, E).astype(np.int32)
+    x = rand_bf16(rng, (T, D))
+    w13 = rand_bf16(rng, (E, 2 * H, D), 0.08)
+    announce(f"swiglu_gather T={T} K={K} E={E} D={D} H={H} {kind}")
+    a, h = ops.grouped_mm_swiglu_gather(bf16_dev(x), torch.from_numpy(sidx).to(DEV), K, bf16_dev(w13),
+                                        _offs(counts), None, save_h=True)
+    h_ref = O.bf16_round(_gmm_ref(x[sidx // K], w13, counts))
+    assert O.max_rel_err(to_np(h), h_ref) < TOL
+    assert O.max_rel_err(to_np(a), O.swiglu(h_ref)) < TOL
+
+
 @pytest.mark.parametrize("topk", [1, 4])
 def test_grouped_mm_unpermute_scatter_scale(ops, topk):
     rng = np.random.default_rng(topk)

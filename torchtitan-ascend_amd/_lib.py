@@ -63,6 +63,11 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i64, _i64, _f32, _c_void_p, _c_void_p, _c_void_p, _sz,
          _c_void_p],
     ),
+    "ttamd_grouped_mm_swiglu_gather": (
+        _i32,
+        [_c_void_p, _i64, _c_void_p, _i32, _c_void_p, _c_void_p, _i64, _i32, _i64, _i64, _f32, _c_void_p,
+         _c_void_p, _c_void_p, _sz, _c_void_p],
+    ),
     "ttamd_grouped_mm_unpermute": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i64, _i64, _c_void_p, _c_void_p, _i64, _c_void_p,

@@ -348,6 +348,33 @@ int ttamd_grouped_mm_swiglu(const void* x, const void* w13, const int32_t* offs,
                    fn);
 }
 
+int ttamd_grouped_mm_swiglu_gather(const void* tokens, int64_t num_tokens, const int32_t* src_index,
+                                   int src_div, const void* w13, const int32_t* offs, int64_t num_rows,
+                                   int num_experts, int64_t hidden, int64_t dim, float swiglu_limit,
+                                   void* a_out, void* h_out, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  const char* fn = "ttamd_grouped_mm_swiglu_gather";
+  TRY(check_gemm_common(fn, offs, num_rows, num_experts));
+  TRY(check_dim(fn, "hidden", hidden, 64));
+  TRY(check_dim(fn, "dim", dim, 64));
+  REQUIRE(dim >= 128, "%s: dim must be >= 128 (got %lld)", fn, (long long)dim);
+  REQUIRE(w13 && aligned16(w13), "%s: w13 must be non-null and 16-byte aligned", fn);
+  REQUIRE(src_div >= 1, "%s: src_div must be >= 1", fn);
+  REQUIRE(num_tokens >= 1 || num_rows == 0, "%s: no token rows", fn);
+  REQUIRE(num_tokens * dim * 2 <= (int64_t)0xffffffffLL, "%s: tokens must stay below 4 GiB", fn);
+  TRY(check_rows(fn, "tokens", tokens, num_tokens, dim));
+  if (num_rows > 0) REQUIRE(src_index != nullptr, "%s: src_index is null", fn);
+  TRY(check_rows(fn, "a_out", a_out, num_rows, hidden));
+  if (h_out) TRY(check_rows(fn, "h_out", h_out, num_rows, 2 * hidden));
+  TRY(check_ws(fn, workspace, workspace_bytes, ttamd::gemm_workspace_bytes(num_rows, num_experts)));
+  if (num_rows == 0) return TTAMD_OK;
+  return check_hip(ttamd::launch_grouped_mm_swiglu_gather(tokens, (int)num_tokens, src_index, src_div, w13,
+                                                          offs, (int)num_rows, num_experts, (int)hidden,
+                                                          (int)dim, swiglu_limit, a_out, h_out, workspace,
+                                                          (hipStream_t)stream),
+                   fn);
+}
+
 int ttamd_grouped_mm_unpermute(const void* a, const void* w2, const int32_t* offs,
                                int64_t num_rows, int num_experts, int64_t dim, int64_t hidden,
                                const float* row_scale, const int32_t* dest, int64_t num_dest_rows,

@@ -569,6 +569,16 @@ hipError_t launch_grouped_mm_swiglu(const void* x, const void* w13, const int* o
   return fwd(EPI_SWIGLU, g, offs, E, M, ws, stream);
 }
 
+hipError_t launch_grouped_mm_swiglu_gather(const void* tokens, int n_tokens, const int* src_index,
+                                           int src_div, const void* w13, const int* offs, int M, int E,
+                                           int H, int D, float limit, void* a_out, void* h_out, void* ws,
+                                           hipStream_t stream) {
+  FwdGemm g = {};
+  g.act = tokens; g.act_index = src_index; g.act_div = src_div; g.n_act = n_tokens;
+  g.w = w13; g.kred = D; g.n = H; g.out = a_out; g.limit = limit; g.h_out = h_out;
+  return fwd(EPI_SWIGLU, g, offs, E, M, ws, stream);
+}
+
 hipError_t launch_grouped_mm_unpermute(const void* act, const void* w2, const int* offs, int M,
                                        int E, int D, int H, const float* row_scale,
                                        const int* dest, int n_dest, void* out, void* ws,

@@ -45,6 +45,9 @@ inline TileTable tile_table_in(void* ws) {
 //   EPI_STORE / EPI_SCATTER: n = N, out [M or n_dest][N].
 struct FwdGemm {
   const void* act;
+  const int* act_index;  // nullable: gathered activation rows (act row = act_index[j] / act_div)
+  int act_div;
+  int n_act;
   const void* w;
   int kred;
   int n;
@@ -60,8 +63,11 @@ struct FwdGemm {
 
 // Kernel arguments of the forward GEMMs (gemm_fwd.hip, gemm_ring.hip).
 struct FwdArgs {
-  const bf16_t* q;  // activations [M][kred]
+  const bf16_t* q;  // activations [M][kred], or [n_q_in][kred] gathered through q_index
   int64_t ldq;
+  const int* q_index;  // nullable: token row j reads q row q_index[j] / q_div
+  int q_div;
+  int n_q_in;
   const bf16_t* p;  // weights, expert e at p + e * p_estride, rows of ldp
   int64_t p_estride;
   int64_t ldp;

@@ -69,7 +69,11 @@ static_assert(TQ % 64 == 0 && TP == 256 && TQ % (8 * WAVES) == 0 && NPB % 2 == 0
 // the tile's first stage into one of three LDS slots (tile round % 3): the
 // slot of round r + 3 is written only after round r's epilogue.
 constexpr int META_BYTES = TQ * 8;
-constexpr int LDS_TOTAL = LDS_BYTES + 3 * META_BYTES;  // 151.5 KB
+// Gathered token rows (q_index): the tile's source-row ids, DMA'd one tile
+// ahead into one of two LDS slots (tile round % 2).
+constexpr int IDX_OFF = LDS_BYTES + 3 * META_BYTES;
+constexpr int IDX_BYTES = TQ * 4;
+constexpr int LDS_TOTAL = IDX_OFF + 2 * IDX_BYTES;  // 154 KB
 static_assert(TQ / 64 <= WAVES, "one 64-row metadata chunk per wave");
 
 // MFMA fragments of one k16 step: NPB weight blocks, NJ token blocks.
@@ -103,6 +107,16 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   const int drow = l >> 3;
 
   // ---- DMA stream -----------------------------------------------------------
+  // Source-row ids of tile round r (gathered rows only): waves 0..TQ/64-1
+  // each move one 64-row chunk into slot r % 2.
+  auto load_ids = [&](int r) {
+    const int tile = r * G + slot;
+    const int4 ti = sload_int4(a.table + tile / a.np_tiles);
+    if (w < TQ / 64) {
+      const uint32_t q = (uint32_t)min(64 * w + l, ti.z - ti.y - 1);
+      dma4(q * 4, (uint64_t)(a.q_index + ti.y), lds0 + IDX_OFF + (uint32_t)((r & 1) * IDX_BYTES) + w * 256);
+    }
+  };
   int d_r = -1;  // tile round whose addresses are loaded
   uint64_t d_pbase = 0, d_qbase = 0;
   uint32_t d_voff[DMA_PER_STAGE];
@@ -127,18 +141,33 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
       }
       d_voff[i] = (uint32_t)(prow * ldp2 + lchunk * 16);
     }
+    if (a.q_index) {
+      // Gathered rows: tile row rr reads source row q_index[row] / q_div,
+      // whose id was DMA'd into LDS while the previous tile was issued.
+      const int* ids = (const int*)(smem + IDX_OFF + (r & 1) * IDX_BYTES);
 #pragma unroll
-    for (int i = 0; i < DMA_Q; ++i) {
-      const int rb = WAVES * i + w;
-      const int rr = 8 * rb + drow;  // tile token row 0..TQ-1
-      const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
-      d_voff[DMA_P + i] = (uint32_t)(min(rr, qmax) * a.ldq * 2 + lchunk * 16);
+      for (int i = 0; i < DMA_Q; ++i) {
+        const int rb = WAVES * i + w;
+        const int rr = 8 * rb + drow;
+        const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
+        const int src = min(max(ids[min(rr, qmax)] / a.q_div, 0), a.n_q_in - 1);
+        d_voff[DMA_P + i] = (uint32_t)(src * a.ldq * 2 + lchunk * 16);
+      }
+      if (r + 1 < nmy) load_ids(r + 1);
+    } else {
+#pragma unroll
+      for (int i = 0; i < DMA_Q; ++i) {
+        const int rb = WAVES * i + w;
+        const int rr = 8 * rb + drow;  // tile token row 0..TQ-1
+        const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
+        d_voff[DMA_P + i] = (uint32_t)(min(rr, qmax) * a.ldq * 2 + lchunk * 16);
+      }
     }
     if constexpr (EPI == EPI_SWIGLU)
       d_pbase = (uint64_t)(a.p + (int64_t)ti.x * a.p_estride + (int64_t)pt * 128 * a.ldp);
     else
       d_pbase = (uint64_t)(a.p + (int64_t)ti.x * a.p_estride + (int64_t)pt * TP * a.ldp);
-    d_qbase = (uint64_t)(a.q + (int64_t)ti.y * a.ldq);
+    d_qbase = (uint64_t)(a.q + (a.q_index ? 0 : (int64_t)ti.y * a.ldq));
     if constexpr (EPI == EPI_SCATTER) {
       if (w < TQ / 64) {
         const uint32_t q = (uint32_t)min(64 * w + l, qmax);
@@ -192,6 +221,10 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   };
 
   // ---- prologue: stages 0 and 1 in flight, fragments of stage 0 / k16 0 read --
+  if (a.q_index) {
+    load_ids(0);
+    wait_vm_barrier<0>();
+  }
   issue(0);
   issue(1);
   wait_vm_barrier<DMA_PER_STAGE>();
@@ -365,6 +398,9 @@ hipError_t launch_fwd_gemm(int epi, const FwdGemm& g, hipStream_t stream) {
   FwdArgs a = {};
   a.q = (const bf16_t*)g.act;
   a.ldq = g.kred;
+  a.q_index = g.act_index;
+  a.q_div = g.act_div > 0 ? g.act_div : 1;
+  a.n_q_in = g.n_act;
   a.p = (const bf16_t*)g.w;
   a.kred = g.kred;
   a.ldp = g.kred;

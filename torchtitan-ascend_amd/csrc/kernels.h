@@ -36,6 +36,10 @@ hipError_t launch_grouped_mm(const void* x, const void* w, const int* offs, int 
 hipError_t launch_grouped_mm_swiglu(const void* x, const void* w13, const int* offs, int M,
                                     int E, int H, int D, float limit, void* a_out, void* h_out,
                                     void* ws, hipStream_t stream);
+hipError_t launch_grouped_mm_swiglu_gather(const void* tokens, int n_tokens, const int* src_index,
+                                           int src_div, const void* w13, const int* offs, int M, int E,
+                                           int H, int D, float limit, void* a_out, void* h_out, void* ws,
+                                           hipStream_t stream);
 hipError_t launch_grouped_mm_unpermute(const void* act, const void* w2, const int* offs, int M,
                                        int E, int D, int H, const float* row_scale,
                                        const int* dest, int n_dest, void* out, void* ws,

@@ -191,13 +191,19 @@ def moe_experts_forward(
     offs = r.offs
     xb = x.to(_BF16).contiguous()
     if not training:
-        mark("permute", False)
-        routed = ops.gather_rows(xb, r.sorted_indices, K, r.sorted_scores if score_before_experts else None)
-        mark("permute", True)
         w13b, w2b = _bf16(w13), _bf16(w2)
-        mark("gemm_w13_swiglu", False)
-        a, _ = ops.grouped_mm_swiglu(routed, w13b, offs, swiglu_limit)
-        mark("gemm_w13_swiglu", True)
+        if score_before_experts or D < 128:
+            mark("permute", False)
+            routed = ops.gather_rows(xb, r.sorted_indices, K, r.sorted_scores if score_before_experts else None)
+            mark("permute", True)
+            mark("gemm_w13_swiglu", False)
+            a, _ = ops.grouped_mm_swiglu(routed, w13b, offs, swiglu_limit)
+            mark("gemm_w13_swiglu", True)
+        else:
+            # the permute gather happens inside the w13 GEMM's loads
+            mark("gemm_w13_swiglu", False)
+            a, _ = ops.grouped_mm_swiglu_gather(xb, r.sorted_indices, K, w13b, offs, swiglu_limit)
+            mark("gemm_w13_swiglu", True)
         scale = None if score_before_experts else r.sorted_scores
         if K == 1:
             mark("gemm_w2_unpermute", False)

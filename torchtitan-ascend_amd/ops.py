@@ -379,6 +379,33 @@ def grouped_mm_swiglu(
     return a, h
 
 
+def grouped_mm_swiglu_gather(
+    tokens: torch.Tensor, src_index: torch.Tensor, src_div: int, w13: torch.Tensor, offs: torch.Tensor,
+    swiglu_limit: float | None = None, save_h: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """grouped_mm_swiglu on the routed rows tokens[src_index[j] // src_div],
+    gathered inside the GEMM's loads (no routed copy)."""
+    dev = _gpu("tokens", tokens)
+    tokens = _want("tokens", tokens, _BF16)
+    src_index = _want("src_index", src_index, torch.int32)
+    w13 = _want("w13", w13, _BF16)
+    offs = _offs(offs, dev)
+    T, D = tokens.shape
+    M = src_index.numel()
+    E, H2, D2 = w13.shape
+    if D2 != D or H2 % 2:
+        raise ValueError(f"w13 must be [E, 2H, {D}], got {tuple(w13.shape)}")
+    H = H2 // 2
+    a = torch.empty(M, H, dtype=_BF16, device=dev)
+    h = torch.empty(M, 2 * H, dtype=_BF16, device=dev) if save_h else None
+    ws = _gemm_ws(M, E, dev)
+    _lib.call(
+        "ttamd_grouped_mm_swiglu_gather", _p(tokens), T, _p(src_index), int(src_div), _p(w13), _p(offs), M, E, H,
+        D, _limit(swiglu_limit), _p(a), _p(h), _p(ws), ws.numel(), _stream(dev),
+    )
+    return a, h
+
+
 def grouped_mm_unpermute(
     a: torch.Tensor,
     w2: torch.Tensor,
