@@ -257,20 +257,21 @@ def main():
 
 
 def time_standalone_permute(ops, router, x, E, K, cfg, reps=20):
-    """Average duration (us) of the permute gather kernel (ttamd_moe_gather_rows)
-    on this workload's routing, on the current stream."""
+    """Average duration (us) of the dispatcher's row permute (ops.permute_rows:
+    ttamd_moe_dispatch_rows for top-k > 1, ttamd_moe_gather_rows for top-1) on
+    this workload's routing, on the current stream."""
     import torch
 
     with torch.no_grad():
         scores, idx = router()
         r = ops.route(idx, E, scores.reshape(-1).float())
-        scale = r.sorted_scores if cfg["score_before"] else None
-        ops.gather_rows(x, r.sorted_indices, K, scale)
+        scale = scores.reshape(-1).float() if cfg["score_before"] else None
+        ops.permute_rows(x, r, K, scale)
         s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         s0.record()
         for _ in range(reps):
-            ops.gather_rows(x, r.sorted_indices, K, scale)
+            ops.permute_rows(x, r, K, scale)
         s1.record()
         torch.cuda.synchronize()
     return s0.elapsed_time(s1) * 1000.0 / reps

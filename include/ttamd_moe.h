@@ -109,6 +109,19 @@ int ttamd_moe_gather_rows(const void* in, const int32_t* src_index,
                           void* out, void* stream);
 
 /*
+ * The permute rows of ttamd_moe_gather_rows in scatter form, from the
+ * inverse map of ttamd_moe_route: out[inverse[t*topk + k]] = tokens[t],
+ * optionally times scores[t*topk + k] in fp32 and rounded to bf16 once
+ * (score before experts).  Identical output to ttamd_moe_gather_rows with
+ * src_index = sorted_indices and row_scale = sorted_scores, but each token
+ * row is read from HBM once.  tokens bf16 [T, D] -> out bf16 [T*topk, D];
+ * topk <= 64.
+ */
+int ttamd_moe_dispatch_rows(const void* tokens, const int32_t* inverse,
+                            const float* scores, int64_t num_tokens,
+                            int64_t hidden, int topk, void* out, void* stream);
+
+/*
  * Drop-in for torch_npu.npu_moe_token_permute(tokens, indices)
  * (torchtitanturbo/models/common/npu_permute.py:74-76): stable sort of the
  * flat labels and gather of token rows.  tokens bf16 [T,D]; labels

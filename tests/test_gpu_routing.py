@@ -142,6 +142,28 @@ def test_gather_rows_score_before_bit_exact(ops):
     np.testing.assert_array_equal(to_np(routed), ref)
 
 
+@pytest.mark.parametrize("T,K,E,D,before", [(1024, 2, 16, 512, True), (777, 8, 128, 2048, False),
+                                             (300, 1, 4, 7168, False), (5, 3, 8, 8, True)])
+def test_dispatch_rows_bit_exact(ops, T, K, E, D, before):
+    """Scatter-form permute from the inverse map: the same routed rows as the
+    gather form and as the oracle (bit-exact), with and without the score."""
+    rng = np.random.default_rng(T + K + D)
+    x = rand_bf16(rng, (T, D))
+    lab = topk_labels(T, K, E, rng)
+    sc = rng.random((T, K)).astype(np.float32)
+    announce(f"dispatch_rows T={T} K={K} D={D} before={before}")
+    r = ops.route(torch.from_numpy(lab).to(DEV), E, f32_dev(sc))
+    xs = bf16_dev(x)
+    routed = ops.dispatch_rows(xs, r.inverse, K, f32_dev(sc.reshape(-1)) if before else None)
+    gathered = ops.gather_rows(xs, r.sorted_indices, K, r.sorted_scores if before else None)
+    assert torch.equal(routed, gathered)
+    sidx = O.stable_order(lab, E)
+    ref = x[sidx // K]
+    if before:
+        ref = O.bf16_round(ref * sc.reshape(-1)[sidx][:, None])
+    np.testing.assert_array_equal(to_np(routed), ref)
+
+
 def test_regroup_permute_matches_reference_semantics(pkg):
     """NpuTokenDispatcher._permute (npu_permute.py:63-85) with synthetic
     (rank, expert) counts: ep=4 ranks x 8 local experts, one GPU."""

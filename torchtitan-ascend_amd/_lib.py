@@ -37,6 +37,7 @@ SIGNATURES: dict[str, tuple] = {
     "ttamd_moe_gather_rows": (
         _i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i32, _c_void_p, _c_void_p]
     ),
+    "ttamd_moe_dispatch_rows": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p]),
     "ttamd_moe_token_permute": (
         _i32,
         [_c_void_p, _c_void_p, _i32, _i64, _i64, _i32, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p,

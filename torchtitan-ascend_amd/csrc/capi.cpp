@@ -229,6 +229,20 @@ int ttamd_moe_combine(const void* permuted, const int32_t* inverse, const float*
                    fn);
 }
 
+int ttamd_moe_dispatch_rows(const void* tokens, const int32_t* inverse, const float* scores,
+                            int64_t num_tokens, int64_t hidden, int topk, void* out, void* stream) {
+  const char* fn = "ttamd_moe_dispatch_rows";
+  TRY(check_hidden(fn, hidden));
+  REQUIRE(topk >= 1 && topk <= 64, "%s: topk must be in [1, 64]", fn);
+  REQUIRE(num_tokens >= 0 && num_tokens * topk <= kI32Max, "%s: num_tokens out of range", fn);
+  TRY(check_rows(fn, "tokens", tokens, num_tokens, hidden));
+  TRY(check_rows(fn, "out", out, num_tokens * topk, hidden));
+  if (num_tokens > 0) REQUIRE(inverse != nullptr, "%s: inverse is null", fn);
+  return check_hip(ttamd::launch_dispatch_rows(tokens, inverse, scores, (int)num_tokens, topk, (int)hidden,
+                                               out, (hipStream_t)stream),
+                   fn);
+}
+
 int ttamd_moe_sum_topk(const void* in, int64_t num_tokens, int64_t hidden, int topk, void* out,
                        void* stream) {
   const char* fn = "ttamd_moe_sum_topk";

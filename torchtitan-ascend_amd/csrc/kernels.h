@@ -17,6 +17,8 @@ hipError_t launch_gather_rows(const void* in, const int* src, const float* scale
                               bool scale_by_src, int n_in, int n_src_max, int rows, int hidden,
                               int div, void* out, hipStream_t stream);
 hipError_t launch_invert_perm(const int* sorted, int M, int* inv, hipStream_t stream);
+hipError_t launch_dispatch_rows(const void* in, const int* inverse, const float* scores, int T, int K,
+                                int hidden, void* out, hipStream_t stream);
 hipError_t launch_combine(const void* in, const int* inverse, const float* probs, int T,
                           int topk, int hidden, void* out, hipStream_t stream);
 hipError_t launch_rowdot(const void* a, const void* b, const int* bidx, int bdiv,

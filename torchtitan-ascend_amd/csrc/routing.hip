@@ -17,6 +17,8 @@
 // Every kernel that indexes memory with device-resident indices clamps them
 // into the valid range, so a corrupt index array yields wrong values, never
 // an out-of-bounds access.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -282,6 +284,68 @@ hipError_t launch_gather_rows(const void* in, const int* src, const float* scale
   hipLaunchKernelGGL(gather_rows_kernel, dim3(move_grid(total)), dim3(kMoveThreads), 0, stream,
                      (const uint4*)in, src, scale, scale_by_src ? 1 : 0, n_in, n_src_max, rows,
                      cpr, div, (uint4*)out);
+  return hipGetLastError();
+}
+
+// Dispatch in scatter form: one wave per token reads its row once and writes
+// the top-k copies, out[inverse[t*K + k]] = x[t] (* scores[t*K + k], rounded
+// to bf16 once).  The same rows as gather_rows with src = sorted order, but x
+// is read once from HBM instead of K times through the caches.
+constexpr int kDispatchUnroll = 4;
+
+__global__ __launch_bounds__(256) void dispatch_rows_kernel(const uint4* __restrict__ in,
+                                                            const int* __restrict__ inverse,
+                                                            const float* __restrict__ scores, int T,
+                                                            int K, int cpr, int M,
+                                                            uint4* __restrict__ out) {
+  const int nw = gridDim.x * 4;
+  const int l = threadIdx.x & 63;
+  for (int t = blockIdx.x * 4 + (threadIdx.x >> 6); t < T; t += nw) {
+    int dst = 0;
+    float sc = 1.f;
+    if (l < K) {
+      dst = min(max(inverse[(int64_t)t * K + l], 0), M - 1);
+      if (scores) sc = scores[(int64_t)t * K + l];
+    }
+    const uint4* irow = in + (int64_t)t * cpr;
+    for (int c0 = 0; c0 < cpr; c0 += 64 * kDispatchUnroll) {
+      uint4 v[kDispatchUnroll];
+#pragma unroll
+      for (int u = 0; u < kDispatchUnroll; ++u) {
+        const int c = c0 + 64 * u + l;
+        if (c < cpr) v[u] = irow[c];
+      }
+      for (int k = 0; k < K; ++k) {
+        const int d = __shfl(dst, k, 64);
+        const float s = __shfl(sc, k, 64);
+        uint4* orow = out + (int64_t)d * cpr;
+#pragma unroll
+        for (int u = 0; u < kDispatchUnroll; ++u) {
+          const int c = c0 + 64 * u + l;
+          if (c < cpr) {
+            uint4 o = v[u];
+            if (scores) {
+              float f[8];
+              unpack8(o, f);
+#pragma unroll
+              for (int i = 0; i < 8; ++i) f[i] *= s;
+              o = pack8(f);
+            }
+            orow[c] = o;
+          }
+        }
+      }
+    }
+  }
+}
+
+hipError_t launch_dispatch_rows(const void* in, const int* inverse, const float* scores, int T, int K,
+                                int hidden, void* out, hipStream_t stream) {
+  if ((int64_t)T * K == 0) return hipSuccess;
+  const int cpr = hidden / 8;
+  const int grid = (int)std::min<int64_t>(((int64_t)T + 3) / 4, 2048);
+  hipLaunchKernelGGL(dispatch_rows_kernel, dim3(grid), dim3(256), 0, stream, (const uint4*)in, inverse,
+                     scores, T, K, cpr, T * K, (uint4*)out);
   return hipGetLastError();
 }
 

@@ -34,7 +34,10 @@ class DispatchFn(torch.autograd.Function):
     def forward(ctx, x, scores_flat, sorted_indices, inverse, sorted_scores, top_k, score_before):
         ctx.top_k = top_k
         ctx.score_before = score_before
-        routed = ops.gather_rows(x, sorted_indices, top_k, sorted_scores if score_before else None)
+        if top_k == 1:
+            routed = ops.gather_rows(x, sorted_indices, 1, sorted_scores if score_before else None)
+        else:
+            routed = ops.dispatch_rows(x, inverse, top_k, scores_flat if score_before else None)
         ctx.save_for_backward(x, scores_flat, sorted_indices, inverse)
         return routed
 
@@ -194,7 +197,7 @@ def moe_experts_forward(
         w13b, w2b = _bf16(w13), _bf16(w2)
         if score_before_experts or D < 128:
             mark("permute", False)
-            routed = ops.gather_rows(xb, r.sorted_indices, K, r.sorted_scores if score_before_experts else None)
+            routed = ops.permute_rows(xb, r, K, scores_flat if score_before_experts else None)
             mark("permute", True)
             mark("gemm_w13_swiglu", False)
             a, _ = ops.grouped_mm_swiglu(routed, w13b, offs, swiglu_limit)

@@ -182,6 +182,38 @@ def gather_rows(
     return out
 
 
+def permute_rows(
+    x: torch.Tensor, r: "RouteResult", top_k: int, scores_flat: torch.Tensor | None = None
+) -> torch.Tensor:
+    """The dispatcher's row permute for a route() result: routed[j] =
+    x[sorted_indices[j] // K] (* score).  top_k > 1 uses the scatter form
+    (each token row read once, K writes); top_k == 1 the gather form
+    (sequential writes), whichever moves fewer HBM bytes."""
+    if top_k == 1:
+        return gather_rows(x, r.sorted_indices, 1, r.sorted_scores if scores_flat is not None else None)
+    return dispatch_rows(x, r.inverse, top_k, scores_flat)
+
+
+def dispatch_rows(
+    x: torch.Tensor, inverse: torch.Tensor, top_k: int, scores_flat: torch.Tensor | None = None
+) -> torch.Tensor:
+    """out[inverse[t*K + k]] = x[t] (* scores_flat[t*K + k], rounded once): the
+    permute rows of gather_rows(x, sorted_indices, K, sorted_scores), with
+    each token row read once."""
+    dev = _gpu("x", x)
+    x = _want("x", x, _BF16)
+    inverse = _want("inverse", inverse, torch.int32)
+    _same_device(dev, inverse=inverse, scores_flat=scores_flat)
+    T, D = x.shape
+    if inverse.numel() != T * top_k:
+        raise ValueError(f"inverse has {inverse.numel()} entries, expected {T * top_k}")
+    if scores_flat is not None:
+        scores_flat = _want("scores_flat", scores_flat, torch.float32)
+    out = torch.empty(T * top_k, D, dtype=_BF16, device=dev)
+    _lib.call("ttamd_moe_dispatch_rows", _p(x), _p(inverse), _p(scores_flat), T, D, top_k, _p(out), _stream(dev))
+    return out
+
+
 def token_permute(
     tokens: torch.Tensor, indices: torch.Tensor, num_experts: int, return_counts: bool = False
 ):
