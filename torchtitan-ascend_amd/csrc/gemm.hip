@@ -655,30 +655,32 @@ hipError_t launch_grouped_mm_fp8_unpermute(const void* aq, const float* sa, cons
   return fp8(EPI_SCATTER, a, offs, E, M, ws, stream);
 }
 
+static hipError_t dgrad(int epi, DgradGemm g, const int* offs, int E, int M, void* ws,
+                        hipStream_t stream) {
+  hipError_t err = launch_tile_map(offs, E, M, kFwdTileRows, ws, stream);
+  if (err != hipSuccess) return err;
+  const TileTable tt = tile_table_in(ws);
+  g.table = tt.table;
+  g.n_qtiles = tt.count;
+  return launch_dgrad_gemm(epi, g, stream);
+}
+
 hipError_t launch_grouped_mm_dgrad(const void* dy, const void* w, const int* offs, int M, int E,
                                    int N, int K, void* dx, void* ws, hipStream_t stream) {
-  // dx[m][k] = sum_n dy[m][n] w[e][n][k]: P index = k (contiguous in w), reduction = n.
-  RowsArgs a = {};
-  a.q = (const bf16_t*)dy; a.ldq = N;
-  a.p = (const bf16_t*)w; a.p_estride = (int64_t)N * K; a.ldp = K;
-  a.kred = N; a.np_tiles = K / BP;
-  a.out = (bf16_t*)dx; a.ldo = K;
-  return launch_rows(EPI_STORE, true, a, offs, E, M, ws, stream);
+  // dx[m][k] = sum_n dy[m][n] w[e][n][k]
+  DgradGemm g = {};
+  g.dy = dy; g.w = w; g.n_red = N; g.n_out = K; g.out = dx;
+  return dgrad(EPI_STORE, g, offs, E, M, ws, stream);
 }
 
 hipError_t launch_grouped_mm_dgrad_swiglu(const void* dy, const void* w2, const void* h,
                                           const int* offs, int M, int E, int D, int H,
                                           float limit, void* dh, void* a_out, void* ws,
                                           hipStream_t stream) {
-  // g[m][p] = sum_d dy[m][d] w2[e][d][p]: P index = p (contiguous in w2), reduction = d.
-  RowsArgs a = {};
-  a.q = (const bf16_t*)dy; a.ldq = D;
-  a.p = (const bf16_t*)w2; a.p_estride = (int64_t)D * H; a.ldp = H;
-  a.kred = D; a.np_tiles = H / BP;
-  a.out = (bf16_t*)dh; a.ldo = 2 * (int64_t)H;
-  a.hidden = H; a.limit = limit; a.h_in = (const bf16_t*)h; a.ldh = 2 * (int64_t)H;
-  a.a_out = (bf16_t*)a_out;
-  return launch_rows(EPI_SWIGLU_BWD, true, a, offs, E, M, ws, stream);
+  // g[m][p] = sum_d dy[m][d] w2[e][d][p], then the SwiGLU backward with h
+  DgradGemm g = {};
+  g.dy = dy; g.w = w2; g.n_red = D; g.n_out = H; g.out = dh; g.h = h; g.limit = limit; g.a_out = a_out;
+  return dgrad(EPI_SWIGLU_BWD, g, offs, E, M, ws, stream);
 }
 
 hipError_t launch_grouped_mm_wgrad(const void* dy, const void* x, const int* offs, int M, int E,

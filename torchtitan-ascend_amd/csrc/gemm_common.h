@@ -83,10 +83,29 @@ struct FwdArgs {
   float limit;  // NaN = no clamp
   bf16_t* h_out;
   int64_t ldh;
+  // EPI_SWIGLU_BWD
+  const bf16_t* h_in;  // saved pre-activation [M][2H]
+  bf16_t* a_out;       // recomputed activation [M][H] (nullable)
   // EPI_SCATTER
   const float* row_scale;
   const int* dest;
   int n_dest;
+};
+
+// Grouped dgrad through the forward kernel's reduction-major weight mode:
+// out[m, k] = sum_n dy[m, n] w[e(m), n, k], w [E, n_red, n_out].
+struct DgradGemm {
+  const void* dy;  // [M][n_red]
+  const void* w;
+  int n_red;
+  int n_out;
+  const int4* table;
+  const int* n_qtiles;
+  void* out;  // EPI_STORE: [M][n_out]; EPI_SWIGLU_BWD: dh [M][2 n_out]
+  // EPI_SWIGLU_BWD
+  const void* h;  // [M][2 n_out]
+  float limit;
+  void* a_out;
 };
 
 // Kernel arguments of the fp8 forward GEMM (gemm_fp8.hip).  Activations and
@@ -128,6 +147,8 @@ hipError_t launch_tile_map(const int* offs, int E, int M, int max_rows, void* ws
                            hipStream_t stream);
 // Forward GEMM over a tile table of at most kFwdTileRows rows per tile.
 hipError_t launch_fwd_gemm(int epi, const FwdGemm& g, hipStream_t stream);
+// dgrad GEMM (EPI_STORE or EPI_SWIGLU_BWD) over the same tile table.
+hipError_t launch_dgrad_gemm(int epi, const DgradGemm& g, hipStream_t stream);
 // fp8 forward GEMM over a tile table of at most kFp8TileRows rows per tile.
 hipError_t launch_fp8_gemm(int epi, const Fp8Args& a, hipStream_t stream);
 

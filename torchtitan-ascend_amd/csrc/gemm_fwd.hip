@@ -76,13 +76,31 @@ constexpr int IDX_BYTES = TQ * 4;
 constexpr int LDS_TOTAL = IDX_OFF + 2 * IDX_BYTES;  // 154 KB
 static_assert(TQ / 64 <= WAVES, "one 64-row metadata chunk per wave");
 
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+
+// Chunk permutation of the 512-byte reduction-major weight rows (PT): the
+// 8 rows n0..n0+3, n0+8..n0+11 one transposed read touches land on four
+// distinct 64-byte bank groups, two rows each.
+__device__ __forceinline__ int ptswz(int n) { return 4 * ((n ^ (n >> 3)) & 3); }
+
 // MFMA fragments of one k16 step: NPB weight blocks, NJ token blocks.
 struct Frag {
   bf16x8_t a[NPB];
   bf16x8_t b[NJ];
 };
 
-template <int EPI>
+// PT (dgrad): the weight operand is reduction-major, w[e][n][k] with the
+// reduction n as rows and the output index k contiguous.  Its stage is 64
+// rows of TP * 2 = 512 bytes (n rows of the tile's 256 output columns), the
+// 16-byte chunk c of row n stored at c ^ ptswz(n), and the MFMA A fragments
+// (8 consecutive n for one output column) come from two
+// ds_read_b64_tr_b16 per block: within each 16-lane group, lane i receives
+// element i % 4 of the 4 loaded by lane 4c + i / 4, for c = 0..3, so lane
+// src points at row n0 + src / 4, columns r0 + 4 (src % 4) .. + 3, and lane
+// i receives rows n0 .. n0 + 3 of column r0 + i.
+// GATHER (inference w13): token row j is q row q_index[j] / q_div.
+template <int EPI, bool PT, bool GATHER>
 __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -129,6 +147,14 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     const int qmax = ti.z - ti.y - 1;
 #pragma unroll
     for (int i = 0; i < DMA_P; ++i) {
+      if constexpr (PT) {
+        // instruction i of wave w: rows 2 (WAVES i + w) and + 1, 32 chunks each
+        const int row = 2 * (WAVES * i + w) + (l >> 5);
+        const int lc = (l & 31) ^ ptswz(row);
+        const int col = min(pt * TP + 8 * lc, a.n_p - 8) - pt * TP;
+        d_voff[i] = (uint32_t)(row * ldp2 + col * 2);
+        continue;
+      }
       const int rb = WAVES * i + w;
       const int rr = 8 * rb + drow;  // tile weight row 0..255
       const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
@@ -141,7 +167,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
       }
       d_voff[i] = (uint32_t)(prow * ldp2 + lchunk * 16);
     }
-    if (a.q_index) {
+    if constexpr (GATHER) {
       // Gathered rows: tile row rr reads source row q_index[row] / q_div,
       // whose id was DMA'd into LDS while the previous tile was issued.
       const int* ids = (const int*)(smem + IDX_OFF + (r & 1) * IDX_BYTES);
@@ -163,11 +189,13 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
         d_voff[DMA_P + i] = (uint32_t)(min(rr, qmax) * a.ldq * 2 + lchunk * 16);
       }
     }
-    if constexpr (EPI == EPI_SWIGLU)
+    if constexpr (PT)
+      d_pbase = (uint64_t)(a.p + (int64_t)ti.x * a.p_estride + (int64_t)pt * TP);
+    else if constexpr (EPI == EPI_SWIGLU)
       d_pbase = (uint64_t)(a.p + (int64_t)ti.x * a.p_estride + (int64_t)pt * 128 * a.ldp);
     else
       d_pbase = (uint64_t)(a.p + (int64_t)ti.x * a.p_estride + (int64_t)pt * TP * a.ldp);
-    d_qbase = (uint64_t)(a.q + (a.q_index ? 0 : (int64_t)ti.y * a.ldq));
+    d_qbase = (uint64_t)(a.q + (GATHER ? 0 : (int64_t)ti.y * a.ldq));
     if constexpr (EPI == EPI_SCATTER) {
       if (w < TQ / 64) {
         const uint32_t q = (uint32_t)min(64 * w + l, qmax);
@@ -183,7 +211,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     const int r = sc / ksteps;
     const int ks = sc - r * ksteps;
     if (r != d_r) dma_tile(r);
-    const uint64_t pb = d_pbase + (uint64_t)ks * ROW_BYTES;
+    const uint64_t pb = d_pbase + (PT ? (uint64_t)ks * TK * a.ldp * 2 : (uint64_t)ks * ROW_BYTES);
     const uint64_t qb = d_qbase + (uint64_t)ks * ROW_BYTES;
     const uint32_t st = lds0 + (uint32_t)((s & 1) * STAGE_BYTES) + w * 1024;
 #pragma unroll
@@ -205,10 +233,38 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     arow[pb] = (EPI == EPI_SWIGLU)
                    ? (pb < NPB / 2 ? (128 / WPN) * wp + 32 * pb : 128 + (128 / WPN) * wp + 32 * (pb - NPB / 2))
                    : (TP / WPN) * wp + 32 * pb;
+  // PT: lane l of 16-lane group g = (l >> 4) & 3 loads row
+  // 16 kk + 8 (g >> 1) + 4 t + (l & 15) / 4, columns arow + 16 (g & 1) +
+  // 4 (l & 3) .. + 3 (t = 0, 1: the two halves of its 8 reduction values).
+  // With n = 16 kk + tr_row + 4 t, ptswz(n) = 4 (bsw ^ 2 (kk & 1)) for a
+  // per-lane bsw, so each (block, kk parity) has one per-lane chunk offset
+  // and kk, t only move the row by constants.
+  const int tr_row = 8 * ((l >> 5) & 1) + ((l & 15) >> 2);
+  const int tr_col = 16 * ((l >> 4) & 1) + 4 * (l & 3);
+  const int bsw = ((l >> 2) & 3) ^ ((l >> 5) & 1);
+  int trx[PT ? NPB : 1][2];
+  if constexpr (PT) {
+#pragma unroll
+    for (int pb = 0; pb < NPB; ++pb)
+#pragma unroll
+      for (int par = 0; par < 2; ++par)
+        trx[pb][par] = tr_row * (TP * 2) + ((tr_col & 4) << 1) +
+                       ((((arow[pb] + tr_col) >> 3) ^ (4 * (bsw ^ (2 * par)))) << 4);
+  }
   auto read_frag = [&](Frag& f, int s, int kk) {
     const char* st = smem + (s & 1) * STAGE_BYTES;
 #pragma unroll
     for (int pb = 0; pb < NPB; ++pb) {
+      if constexpr (PT) {
+        short4_t v[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int off = trx[pb][kk & 1] + (16 * kk + 4 * t) * (TP * 2);
+          v[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(st + off));
+        }
+        f.a[pb] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
+        continue;
+      }
       const int pc = (2 * kk + half) ^ fa ^ (4 * ((arow[pb] >> 5) & 1));
       f.a[pb] = *(const bf16x8_t*)(st + (arow[pb] + r32) * ROW_BYTES + pc * 16);
     }
@@ -221,7 +277,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   };
 
   // ---- prologue: stages 0 and 1 in flight, fragments of stage 0 / k16 0 read --
-  if (a.q_index) {
+  if constexpr (GATHER) {
     load_ids(0);
     wait_vm_barrier<0>();
   }
@@ -286,6 +342,20 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     //      loop, where every register is taken.
     int er32 = r32;
     asm volatile("" : "+v"(er32));
+    // EPI_SWIGLU_BWD: saved pre-activation of token block jj
+    auto load_h = [&](int jj, int pb, uint2 (&dst)[4][2]) {
+      if constexpr (EPI == EPI_SWIGLU_BWD) {
+        const int gq = row0 + NJ * 32 * wq + 32 * jj + er32;
+        const int qrow = min(gq, row1 - 1);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = min(pt * TP + arow[pb], a.n_p - 32) + 8 * g + 4 * half;
+          const bf16_t* hrow = a.h_in + (int64_t)qrow * a.ldh + col;
+          dst[g][0] = *(const uint2*)hrow;
+          dst[g][1] = *(const uint2*)(hrow + a.hidden);
+        }
+      }
+    };
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int gq = row0 + NJ * 32 * wq + 32 * j + er32;
@@ -326,6 +396,56 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
             __builtin_amdgcn_sched_barrier(0);
           }
         }
+      } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+        // acc = dA = g for output columns p of the activation; with the saved
+        // bf16 pre-activation h = [gate | up]: dgate, dup (clamp masks from
+        // the bf16 h, as the reference's autograd sees them).  The 8 h values
+        // of a 32-column block are loaded before any is used.
+        const bool clamp = (a.limit == a.limit);
+        const float L = a.limit;
+#pragma unroll
+        for (int pb = 0; pb < NPB; ++pb) {
+          uint2 hv[4][2];
+          load_h(j, pb, hv);
+          if (pt * TP + arow[pb] < a.n_p && row_ok) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const int col = pt * TP + arow[pb] + 8 * g + 4 * half;
+              const uint2 hg = hv[g][0];
+              const uint2 hu = hv[g][1];
+              const float gate[4] = {bf16_to_f32(hg.x & 0xffff), bf16_to_f32(hg.x >> 16),
+                                     bf16_to_f32(hg.y & 0xffff), bf16_to_f32(hg.y >> 16)};
+              const float up[4] = {bf16_to_f32(hu.x & 0xffff), bf16_to_f32(hu.x >> 16),
+                                   bf16_to_f32(hu.y & 0xffff), bf16_to_f32(hu.y >> 16)};
+              float dg[4], du[4], av[4];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const float gd = acc[pb][j][4 * g + i];
+                float gc = gate[i], uc = up[i];
+                float mg = 1.f, mu = 1.f;
+                if (clamp) {
+                  if (gc > L) { gc = L; mg = 0.f; }
+                  if (uc > L) { uc = L; mu = 0.f; }
+                  if (uc < -L) { uc = -L; mu = 0.f; }
+                }
+                const float sig = 1.f / (1.f + __expf(-gc));
+                const float sv = gc * sig;
+                const float ds = sig * (1.f + gc * (1.f - sig));
+                dg[i] = gd * uc * ds * mg;
+                du[i] = gd * sv * mu;
+                av[i] = sv * uc;
+              }
+              bf16_t* drow = a.out + (int64_t)gq * a.ldo + col;
+              *(uint2*)drow = make_uint2(pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3]));
+              *(uint2*)(drow + a.hidden) = make_uint2(pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3]));
+              if (a.a_out) {
+                bf16_t* arow_p = a.a_out + (int64_t)gq * a.hidden + col;
+                *(uint2*)arow_p = make_uint2(pack_bf16x2(av[0], av[1]), pack_bf16x2(av[2], av[3]));
+              }
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
       } else {
         float sc = 1.f;
         int orow_idx = gq;
@@ -365,17 +485,17 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   wait_vm<0>();  // DMAs past the end have landed before the workgroup exits
 }
 
-template <int EPI>
+template <int EPI, bool PT = false, bool GATHER = false>
 hipError_t launch_fwd(FwdArgs a, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t err = hipFuncSetAttribute((const void*)gg_fwd_kernel<EPI>,
+    hipError_t err = hipFuncSetAttribute((const void*)gg_fwd_kernel<EPI, PT, GATHER>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize, LDS_TOTAL);
     if (err != hipSuccess) return err;
     attr_set = true;
   }
   const int grid = (num_cus() + 7) & ~7;
-  hipLaunchKernelGGL(gg_fwd_kernel<EPI>, dim3(grid), dim3(FTHREADS), LDS_TOTAL, stream, a);
+  hipLaunchKernelGGL((gg_fwd_kernel<EPI, PT, GATHER>), dim3(grid), dim3(FTHREADS), LDS_TOTAL, stream, a);
   return hipGetLastError();
 }
 
@@ -416,6 +536,7 @@ hipError_t launch_fwd_gemm(int epi, const FwdGemm& g, hipStream_t stream) {
     a.limit = g.limit;
     a.h_out = (bf16_t*)g.h_out;
     a.ldh = 2 * (int64_t)g.n;
+    if (a.q_index) return launch_fwd<EPI_SWIGLU, false, true>(a, stream);
     return launch_fwd<EPI_SWIGLU>(a, stream);
   }
   a.p_estride = (int64_t)g.n * g.kred;
@@ -427,6 +548,35 @@ hipError_t launch_fwd_gemm(int epi, const FwdGemm& g, hipStream_t stream) {
   a.n_dest = g.n_dest;
   if (epi == EPI_SCATTER) return launch_fwd<EPI_SCATTER>(a, stream);
   return launch_fwd<EPI_STORE>(a, stream);
+}
+
+hipError_t launch_dgrad_gemm(int epi, const DgradGemm& g, hipStream_t stream) {
+  // out[m, k] = sum_n dy[m, n] w[e, n, k]: token rows q = dy (reduction n
+  // contiguous), weight operand w[e] = [n][k] reduction-major.
+  FwdArgs a = {};
+  a.q = (const bf16_t*)g.dy;
+  a.ldq = g.n_red;
+  a.q_div = 1;
+  a.p = (const bf16_t*)g.w;
+  a.p_estride = (int64_t)g.n_red * g.n_out;
+  a.ldp = g.n_out;
+  a.kred = g.n_red;
+  a.n_p = g.n_out;
+  a.np_tiles = (g.n_out + TP - 1) / TP;
+  a.table = g.table;
+  a.n_qtiles = g.n_qtiles;
+  a.out = (bf16_t*)g.out;
+  if (epi == EPI_SWIGLU_BWD) {
+    a.ldo = 2 * (int64_t)g.n_out;
+    a.hidden = g.n_out;
+    a.limit = g.limit;
+    a.h_in = (const bf16_t*)g.h;
+    a.ldh = 2 * (int64_t)g.n_out;
+    a.a_out = (bf16_t*)g.a_out;
+    return launch_fwd<EPI_SWIGLU_BWD, true>(a, stream);
+  }
+  a.ldo = g.n_out;
+  return launch_fwd<EPI_STORE, true>(a, stream);
 }
 
 }  // namespace ttamd
