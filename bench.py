@@ -144,6 +144,8 @@ def main():
         xg = x.clone().requires_grad_(True)
 
         def step(ev=None):
+            # a training step starts from cleared gradients (zero_grad(set_to_none=True))
+            w13p.grad = w2p.grad = xg.grad = None
             scores, idx = router()
             scores = scores.detach().requires_grad_(True)
             out = F.moe_experts_forward(xg, scores, idx, w13p, w2p, E, cfg["score_before"])

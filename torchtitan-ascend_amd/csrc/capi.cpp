@@ -469,6 +469,8 @@ int ttamd_grouped_mm_wgrad(const void* dy, const void* x, const int32_t* offs, i
   REQUIRE(dw && aligned16(dw), "%s: dw must be non-null and 16-byte aligned", fn);
   REQUIRE((int64_t)num_experts * n * k <= (int64_t)1 << 40, "%s: dw too large", fn);
   REQUIRE((int64_t)num_experts * (n / 128) * (k / 128) <= kI32Max, "%s: too many tiles", fn);
+  REQUIRE(num_rows * n * 2 <= (int64_t)0xffffffffLL && num_rows * k * 2 <= (int64_t)0xffffffffLL,
+          "%s: dy and x must each stay below 4 GiB", fn);
   return check_hip(ttamd::launch_grouped_mm_wgrad(dy, x, offs, (int)num_rows, num_experts, (int)n,
                                                   (int)k, dw, dw_is_fp32 != 0,
                                                   (hipStream_t)stream),

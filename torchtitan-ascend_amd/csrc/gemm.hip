@@ -685,17 +685,13 @@ hipError_t launch_grouped_mm_dgrad_swiglu(const void* dy, const void* w2, const 
 
 hipError_t launch_grouped_mm_wgrad(const void* dy, const void* x, const int* offs, int M, int E,
                                    int N, int K, void* dw, bool fp32, hipStream_t stream) {
-  WgradArgs a = {};
+  WgradDmaArgs a = {};
   a.dy = (const bf16_t*)dy; a.lddy = N;
   a.x = (const bf16_t*)x; a.ldx = K;
-  a.offs = offs; a.E = E; a.M = M;
-  a.n_tiles = N / 128; a.k_tiles = K / 128;
+  a.offs = offs; a.E = E; a.M = M; a.N = N; a.K = K;
+  a.n_tiles = (N + 255) / 256; a.k_tiles = (K + 255) / 256;
   a.dw = dw; a.dw_fp32 = fp32 ? 1 : 0;
-  a.N = N; a.K = K;
-  const int grid = round_up8(E * a.n_tiles * a.k_tiles);
-  a.grid_per_xcd = grid / 8;
-  hipLaunchKernelGGL(gg_wgrad_kernel, dim3(grid), dim3(kGemmThreads), 0, stream, a);
-  return hipGetLastError();
+  return launch_wgrad_dma(a, stream);
 }
 
 }  // namespace ttamd

@@ -108,6 +108,21 @@ struct DgradGemm {
   void* a_out;
 };
 
+// Grouped weight gradient (gemm_wgrad.hip): dw[e][n][k] = sum over the
+// expert's rows m of dy[m][n] * x[m][k].
+struct WgradDmaArgs {
+  const bf16_t* dy;  // [M][N]
+  int64_t lddy;
+  const bf16_t* x;  // [M][K]
+  int64_t ldx;
+  const int* offs;  // inclusive, [E]
+  int E, M, N, K;
+  int n_tiles, k_tiles;  // per expert, 256-wide
+  void* dw;              // [E][N][K]
+  int dw_fp32;
+};
+hipError_t launch_wgrad_dma(const WgradDmaArgs& a, hipStream_t stream);
+
 // Kernel arguments of the fp8 forward GEMM (gemm_fp8.hip).  Activations and
 // weights are e4m3 bytes; strides are in bytes for them, in elements for
 // the scale and output arrays.

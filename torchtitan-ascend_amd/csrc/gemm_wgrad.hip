@@ -1,0 +1,273 @@
+// Persistent grouped weight gradient on MI355X (gfx950):
+//
+//   dw[e][n][k] = sum_{m in rows(e)} dy[m][n] * x[m][k]
+//
+// The backward of torch._grouped_mm w.r.t. its weight (npu_gmm.py:31, :38
+// under autograd): dw13 = dh^T x, dw2 = dy^T a per expert, reduction over the
+// expert's ragged row range.
+//
+// Both operands are reduction-major (rows m, columns contiguous), so the
+// MFMA fragments (8 consecutive m per lane) come from ds_read_b64_tr_b16 on
+// the rows exactly as they arrive from HBM:
+//   * Tile: 256 output rows n (the MFMA B operand, one n per lane) x 256
+//     output columns k (A operand, 4 consecutive k per lane and register
+//     group, so fp32 / bf16 results leave as 16- / 8-byte stores).
+//   * 8 waves (2 per SIMD), 2 (n) x 4 (k); each wave 128 n x 64 k =
+//     2 x 4 accumulators of v_mfma_f32_32x32x16_bf16.
+//   * Stages of 64 rows m: x rows (64 x 512 bytes) and dy rows (64 x 512
+//     bytes) DMA'd by global_load_lds_dwordx4 into two 64 KB buffers, chunk
+//     c of row m stored at c ^ 4 ((m ^ (m >> 3)) & 3) (conflict-free
+//     transposed reads); one barrier per stage as in gemm_fwd.hip.
+//   * The last stage of an expert reads clamped rows past its end; their
+//     products are removed by zeroing those rows in the x fragments.
+//   * Persistent over (expert, n tile, k tile), expert-major, with the
+//     XCD-aware slot mapping of gemm_fwd.hip; the DMA stream runs over the
+//     flattened (tile, stage) sequence, whose stage counts vary per expert.
+//     An expert without rows still takes one (fully masked) stage, so its
+//     gradient tile is written as zeros.
+#include "common.h"
+#include "dma_asm.h"
+#include "gemm_common.h"
+#include "kernels.h"
+
+namespace ttamd {
+namespace {
+
+using namespace dma;
+
+constexpr int TQ = 256;  // n per tile
+constexpr int TP = 256;  // k per tile
+constexpr int TK = 64;   // rows m per stage
+constexpr int WAVES = 8;
+constexpr int WPN = 4;              // waves along k
+constexpr int NJ = TQ / 32 / 2;     // 4 n blocks per wave
+constexpr int NPB = TP / 32 / WPN;  // 2 k blocks per wave
+constexpr int THREADS = 64 * WAVES;
+constexpr int ROW_BYTES = 512;      // 256 bf16 columns of one row m
+constexpr int OP_BYTES = TK * ROW_BYTES;  // 32 KB per operand and stage
+constexpr int STAGE_BYTES = 2 * OP_BYTES;
+constexpr int LDS_BYTES = 2 * STAGE_BYTES;  // 128 KB
+constexpr int DMA_OP = OP_BYTES / 1024 / WAVES;  // 4 instructions per operand and wave
+constexpr int DMA_PER_STAGE = 2 * DMA_OP;
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+
+__device__ __forceinline__ int ptswz(int m) { return 4 * ((m ^ (m >> 3)) & 3); }
+
+struct Frag {
+  bf16x8_t a[NPB];  // x: k blocks
+  bf16x8_t b[NJ];   // dy: n blocks
+};
+
+__global__ __launch_bounds__(THREADS, 1) void gg_wgrad_dma_kernel(const WgradDmaArgs a) {
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wq = w / WPN;
+  const int wp = w % WPN;
+  const int l = threadIdx.x & 63;
+  const int G = gridDim.x;
+  const int b = blockIdx.x;
+  const int slot = (b & 7) * (G >> 3) + (b >> 3);
+  const int per_e = a.n_tiles * a.k_tiles;
+  const int ntiles = a.E * per_e;
+  const int nmy = slot < ntiles ? (ntiles - slot + G - 1) / G : 0;
+  if (nmy == 0) return;
+  const uint32_t lds0 = lds_addr(smem);
+
+  // tile round r -> (expert, n tile, k tile, first row, end row, stages)
+  struct Tile {
+    int e, nt, kt, m0, m1, nks;
+  };
+  auto tile_of = [&](int r) {
+    Tile t;
+    const int id = r * G + slot;
+    t.e = id / per_e;
+    const int rem = id - t.e * per_e;
+    t.nt = rem / a.k_tiles;
+    t.kt = rem - t.nt * a.k_tiles;
+    t.m0 = t.e == 0 ? 0 : sload_int(a.offs + t.e - 1);
+    t.m1 = sload_int(a.offs + t.e);
+    t.m0 = min(max(t.m0, 0), a.M);
+    t.m1 = min(max(t.m1, t.m0), a.M);
+    t.nks = max(1, (t.m1 - t.m0 + TK - 1) / TK);
+    return t;
+  };
+
+  // ---- DMA stream: a cursor over (tile round, stage) --------------------------
+  // instruction i of wave w moves rows 2 (WAVES i + w) and + 1 of an operand;
+  // lane l: row + (l >> 5), physical chunk l & 31.
+  int c_r = 0, c_ks = 0;
+  Tile c_t = tile_of(0);
+  auto issue = [&](int s) {
+    const int m_stage = c_t.m0 + TK * c_ks;
+    const int nvalid = c_t.m1 - m_stage;  // may be <= 0 for an expert without rows
+    const uint64_t xb = (uint64_t)(a.x + (int64_t)c_t.kt * TP);
+    const uint64_t yb = (uint64_t)(a.dy + (int64_t)c_t.nt * TQ);
+    const uint32_t st = lds0 + (uint32_t)((s & 1) * STAGE_BYTES) + w * 1024;
+    if (a.M > 0) {  // no rows at all: every stage is masked, nothing to load
+#pragma unroll
+    for (int i = 0; i < DMA_OP; ++i) {
+      const int row = 2 * (WAVES * i + w) + (l >> 5);
+      const int lc = (l & 31) ^ ptswz(row);
+      const int m = min(max(m_stage + min(row, nvalid - 1), 0), a.M - 1);
+      const int xcol = min(c_t.kt * TP + 8 * lc, a.K - 8) - c_t.kt * TP;
+      dma16((uint32_t)(m * a.ldx * 2 + xcol * 2), xb, st + i * (WAVES * 1024));
+    }
+#pragma unroll
+    for (int i = 0; i < DMA_OP; ++i) {
+      const int row = 2 * (WAVES * i + w) + (l >> 5);
+      const int lc = (l & 31) ^ ptswz(row);
+      const int m = min(max(m_stage + min(row, nvalid - 1), 0), a.M - 1);
+      const int ycol = min(c_t.nt * TQ + 8 * lc, a.N - 8) - c_t.nt * TQ;
+      dma16((uint32_t)(m * a.lddy * 2 + ycol * 2), yb, st + OP_BYTES + i * (WAVES * 1024));
+    }
+    }
+    // advance; past the last stage keep re-loading it
+    if (c_ks + 1 < c_t.nks) {
+      ++c_ks;
+    } else if (c_r + 1 < nmy) {
+      ++c_r;
+      c_ks = 0;
+      c_t = tile_of(c_r);
+    }
+  };
+
+  // ---- fragments: transposed reads (see gemm_fwd.hip, PT) ---------------------
+  const int tr_row = 8 * ((l >> 5) & 1) + ((l & 15) >> 2);
+  const int tr_col = 16 * ((l >> 4) & 1) + 4 * (l & 3);
+  const int bsw = ((l >> 2) & 3) ^ ((l >> 5) & 1);
+  int arow[NPB], brow[NJ];
+#pragma unroll
+  for (int pb = 0; pb < NPB; ++pb) arow[pb] = (TP / WPN) * wp + 32 * pb;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) brow[j] = (TQ / 2) * wq + 32 * j;
+  // Offset of the lane's 8-byte piece for a 32-column block at col0 (uniform)
+  // and reduction rows 16 kk + 4 t + tr_row: the chunk XOR depends on the
+  // lane and on kk & 1 only (see gemm_fwd.hip, PT).
+  const int tr_base = tr_row * ROW_BYTES + ((tr_col & 4) << 1);
+  const int tc8 = tr_col >> 3;
+  const int swz0 = 4 * bsw, swz1 = 4 * (bsw ^ 2);
+  auto tr8 = [&](const char* st, int col0, int kk) {
+    const int off = tr_base + ((((col0 >> 3) + tc8) ^ ((kk & 1) ? swz1 : swz0)) << 4) + (16 * kk) * ROW_BYTES;
+    short4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(st + off));
+    short4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t*)(st + off + 4 * ROW_BYTES));
+    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+  auto read_frag = [&](Frag& f, int s, int kk) {
+    const char* st = smem + (s & 1) * STAGE_BYTES;
+#pragma unroll
+    for (int pb = 0; pb < NPB; ++pb) f.a[pb] = tr8(st, arow[pb], kk);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) f.b[j] = tr8(st + OP_BYTES, brow[j], kk);
+  };
+  // Rows >= nvalid of a stage contribute nothing: zero them in the x
+  // fragments.  Lane l holds rows 16 kk + 8 (l >> 5) + {0..3} and + 4 + {0..3}.
+  auto mask_frag = [&](Frag& f, int kk, int nvalid) {
+    // element i of the lane's 8 is row 16 kk + 8 (l >> 5) + i: kept if i < rem
+    const int rem = nvalid - 16 * kk - 8 * ((l >> 5) & 1);
+#pragma unroll
+    for (int pb = 0; pb < NPB; ++pb) {
+      u32x4_t v = __builtin_bit_cast(u32x4_t, f.a[pb]);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint32_t keep = (2 * d < rem ? 0x0000ffffu : 0u) | (2 * d + 1 < rem ? 0xffff0000u : 0u);
+        v[d] &= keep;
+      }
+      f.a[pb] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  };
+
+  // ---- prologue --------------------------------------------------------------
+  issue(0);
+  issue(1);
+  wait_vm_barrier<DMA_PER_STAGE>();
+  Frag f0, f1;
+  read_frag(f0, 0, 0);
+
+  int s = 0;
+  for (int r = 0; r < nmy; ++r) {
+    const Tile t = tile_of(r);
+    floatx16_t acc[NPB][NJ];
+#pragma unroll
+    for (int i = 0; i < NPB; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+    auto mfma = [&](const Frag& f) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int pb = 0; pb < NPB; ++pb)
+          acc[pb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[pb], f.b[j], acc[pb][j], 0, 0, 0);
+    };
+    for (int ks = 0; ks < t.nks; ++ks, ++s) {
+      const int nvalid = t.m1 - (t.m0 + TK * ks);
+      const bool partial = nvalid < TK;  // wave-uniform
+      if (partial) mask_frag(f0, 0, nvalid);
+      read_frag(f1, s, 1);
+      if (partial) mask_frag(f1, 1, nvalid);
+      mfma(f0);
+      read_frag(f0, s, 2);
+      if (partial) mask_frag(f0, 2, nvalid);
+      mfma(f1);
+      read_frag(f1, s, 3);
+      if (partial) mask_frag(f1, 3, nvalid);
+      mfma(f0);
+      wait_vm_barrier<0>();  // stage s + 1 landed, every wave done with stage s
+      issue(s + 2);
+      read_frag(f0, s + 1, 0);
+      mfma(f1);
+    }
+
+    // ---- epilogue: acc[pb][j][4g + i] = dw[e][n][k], n = nt*TQ + brow[j] +
+    //      lane % 32, k = kt*TP + arow[pb] + 8g + 4 (lane / 32) + i.
+    int er32 = l & 31;
+    asm volatile("" : "+v"(er32));
+    const int half = l >> 5;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int n = t.nt * TQ + brow[j] + er32;
+      const bool n_ok = n < a.N;
+      const int64_t rowoff = ((int64_t)t.e * a.N + n) * a.K;
+#pragma unroll
+      for (int pb = 0; pb < NPB; ++pb) {
+        if (t.kt * TP + arow[pb] < a.K) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int k = t.kt * TP + arow[pb] + 8 * g + 4 * half;
+            const floatx16_t& v = acc[pb][j];
+            if (n_ok) {
+              if (a.dw_fp32) {
+                *(float4*)((float*)a.dw + rowoff + k) = make_float4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
+              } else {
+                *(uint2*)((bf16_t*)a.dw + rowoff + k) =
+                    make_uint2(pack_bf16x2(v[4 * g], v[4 * g + 1]), pack_bf16x2(v[4 * g + 2], v[4 * g + 3]));
+              }
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  wait_vm<0>();
+}
+
+}  // namespace
+
+hipError_t launch_wgrad_dma(const WgradDmaArgs& a, hipStream_t stream) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t err = hipFuncSetAttribute((const void*)gg_wgrad_dma_kernel,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+    if (err != hipSuccess) return err;
+    attr_set = true;
+  }
+  const int grid = (num_cus() + 7) & ~7;
+  hipLaunchKernelGGL(gg_wgrad_dma_kernel, dim3(grid), dim3(THREADS), LDS_BYTES, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace ttamd
