@@ -36,8 +36,9 @@ CONFIGS = {
                norm=False, score_before=True, backward=False),
     "c2": dict(name="C2 Qwen3-30B-A3B MoE layer forward", T=8192, D=2048, H=768, E=128, K=8, router="softmax",
                norm=True, score_before=False, backward=False),
-    "c3": dict(name="C3 Llama4-Scout MoE layer forward+backward (routed experts)", T=8192, D=5120, H=8192, E=16,
-               K=1, router="sigmoid", norm=False, score_before=True, backward=True),
+    "c3": dict(name="C3 Llama4-Scout MoE layer forward+backward (16 routed experts + 1 shared expert)", T=8192,
+               D=5120, H=8192, E=16, K=1, router="sigmoid", norm=False, score_before=True, backward=True,
+               shared=True),
     "c4": dict(name="C4 DeepSeek-V3 expert shard forward (Zipf 1.2)", T=32768, D=7168, H=2048, E=32, K=1,
                router="zipf", norm=False, score_before=False, backward=False),
     "c5": dict(name="C5 DeepSeek-V3 expert shard forward, fp8 e4m3 experts (128x128 weight scales, "
@@ -142,6 +143,13 @@ def main():
         w2p = w2.clone().requires_grad_(True)
         dout = torch.randn(T, D, device=dev).to(torch.bfloat16)
         xg = x.clone().requires_grad_(True)
+        shared = cfg.get("shared", False)
+        if shared:
+            # the always-on shared expert: the same SwiGLU FFN on every token,
+            # run as a one-expert grouped GEMM
+            sw13 = (torch.randn(1, 2 * H, D, device=dev) * 0.02).to(torch.bfloat16).requires_grad_(True)
+            sw2 = (torch.randn(1, D, H, device=dev) * 0.02).to(torch.bfloat16).requires_grad_(True)
+            all_tokens = torch.full((1,), T, dtype=torch.int32, device=dev)
 
         def step(ev=None):
             # a training step starts from cleared gradients (zero_grad(set_to_none=True))
@@ -149,6 +157,9 @@ def main():
             scores, idx = router()
             scores = scores.detach().requires_grad_(True)
             out = F.moe_experts_forward(xg, scores, idx, w13p, w2p, E, cfg["score_before"])
+            if shared:
+                sw13.grad = sw2.grad = None
+                out = out + F.run_experts_grouped_mm(sw13, sw2, xg, all_tokens)
             out.backward(dout)
             return out
     else:
@@ -211,7 +222,7 @@ def main():
     permute_gbs = permute_bytes / (permute_us * 1e-6) / 1e9
     peak = PEAK_FP8_TFLOPS if fp8 else PEAK_BF16_TFLOPS
 
-    fwd_flops = 6.0 * M * D * H
+    fwd_flops = 6.0 * M * D * H + (6.0 * T * D * H if cfg.get("shared") else 0.0)
     total_flops = fwd_flops * (3 if cfg["backward"] else 1)
     tokens_per_s = T / (ms * 1e-3)
     result = {
