@@ -252,6 +252,8 @@ def main():
         "stage_us": {k: round(v, 2) for k, v in stage_us.items()},
         "roofline": {
             "kernel": ("gg_fp8_kernel<EPI_SWIGLU> (fp8 grouped GEMM w13 + SwiGLU epilogue)" if fp8 else
+                       "gg_fwd_kernel<EPI_SWIGLU, GATHER> (permute gather + grouped GEMM w13 + SwiGLU epilogue)"
+                       if not cfg["score_before"] else
                        "gg_fwd_kernel<EPI_SWIGLU> (grouped GEMM w13 + SwiGLU epilogue)"),
             "bound": "mfma",
             "achieved": round(w13_tflops, 1),
