@@ -15,15 +15,18 @@
 // (one scale block, one 128-byte line per row).
 //   * 4 waves, one per SIMD, 2 x 2: wave (wq, wp) owns token rows 128wq.. and
 //     64 weight rows (SWIGLU: 32 gate rows and the 32 matching up rows), i.e.
-//     2 x 4 blocks of v_mfma_scale_f32_32x32x64_f8f6f4 (unit hardware
-//     scales).  Each block's k = 128 partial sum is kept apart (2 MFMAs) and
-//     added into the fp32 accumulator times sx * sw, so the fp32 block
-//     scales are applied exactly once per block as in the dequantised form.
+//     4 x 8 blocks of v_mfma_scale_f32_16x16x128_f8f6f4 (unit hardware
+//     scales): one MFMA covers a block's whole k = 128 scale block, and its
+//     partial sum goes straight into the fp32 accumulator times sx * sw, so
+//     the fp32 block scales are applied once per block as in the dequantised
+//     form, with no partial sums kept across MFMAs.
 //   * Three LDS stages of 50 KB: 16 KB weight rows + 32 KB token rows (DMA,
 //     global_load_lds_dwordx4, 8 rows per instruction, XOR-swizzled 16-byte
 //     chunks as in the bf16 kernel), 1 KB of token-row scales and one copy of
-//     the stage's weight-block scales per wave.  Two stages are in flight
-//     while the third is consumed.
+//     the stage's weight-block scales per wave.  The barrier at the top of
+//     stage s waits for stage s + 1, so while stage s is computed from
+//     registers, each fragment register is refilled with stage s + 1 right
+//     after its last use.
 //   * Persistent workgroups, XCD-aware slots, flattened (tile, stage) DMA
 //     stream and the EPI_SCATTER metadata in LDS follow gemm_fwd.hip.
 #include "common.h"
@@ -66,11 +69,13 @@ typedef int i32x8_t __attribute__((ext_vector_type(8)));
 // Chunk permutation of 128-byte LDS rows (as in gemm_fwd.hip).
 __device__ __forceinline__ int cswz(int r) { return (r ^ (r >> 3)) & 7; }
 
-// Fragments of one k64 step: NPB weight blocks, NJ token blocks, 32 bytes
-// (32 e4m3 values) per lane each.
-struct Frag8 {
-  i32x8_t a[NPB];
-  i32x8_t b[NJ];
+// Fragments of one stage (k = 128): NPB16 weight blocks and NJ16 token
+// blocks of 16 rows; lane l holds bytes 32 (l / 16) .. + 31 of row l % 16.
+constexpr int NPB16 = 4;
+constexpr int NJ16 = 8;
+struct Frag16 {
+  i32x8_t a[NPB16];
+  i32x8_t b[NJ16];
 };
 
 template <int EPI>
@@ -162,57 +167,51 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
   };
 
   // ---- fragment geometry -------------------------------------------------------
-  const int r32 = l & 31;
-  const int half = l >> 5;
-  const int fa = cswz(r32);
-  int arow[NPB];
+  const int r16 = l & 15;
+  const int g4 = l >> 4;
+  const int f16 = cswz(r16);  // cswz(16m + r16) = f16 ^ 2 (m & 3 ... see arow)
+  int arow[NPB16];  // weight block starts (tile rows)
 #pragma unroll
-  for (int pb = 0; pb < NPB; ++pb)
-    arow[pb] = (EPI == EPI_SWIGLU) ? 32 * wp + 64 * pb : 64 * wp + 32 * pb;
-  // k64 step `sub` of a stage: lane (r32, half) takes bytes 64sub + 32half ..
-  // + 31 of its row, logical chunks c0 = 4sub + 2half and c0 + 1.
-  auto read_frag = [&](Frag8& f, int s, int sub) {
-    const char* st = smem + (s % NSTAGE) * STAGE_BYTES;
-    const int c0 = 4 * sub + 2 * half;
-#pragma unroll
-    for (int pb = 0; pb < NPB; ++pb) {
-      const int m = arow[pb] >> 5;
-      const int x = fa ^ (4 * (m & 1));
-      const char* row = st + (arow[pb] + r32) * TKB;
-      const i32x4_t lo = *(const i32x4_t*)(row + ((c0 ^ x) * 16));
-      const i32x4_t hi = *(const i32x4_t*)(row + (((c0 + 1) ^ x) * 16));
-      f.a[pb] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    }
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int m = 4 * wq + j;
-      const int x = fa ^ (4 * (m & 1));
-      const char* row = st + P_BYTES + (32 * m + r32) * TKB;
-      const i32x4_t lo = *(const i32x4_t*)(row + ((c0 ^ x) * 16));
-      const i32x4_t hi = *(const i32x4_t*)(row + (((c0 + 1) ^ x) * 16));
-      f.b[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    }
+  for (int pb = 0; pb < NPB16; ++pb)
+    arow[pb] = (EPI == EPI_SWIGLU) ? (pb < 2 ? 32 * wp + 16 * pb : 64 + 32 * wp + 16 * (pb - 2))
+                                   : 64 * wp + 16 * pb;
+  // Row 16m + r16 of a 128-byte-row operand: cswz = f16 ^ ((2m) & 6) (16m >> 3
+  // = 2m is even, so adding r16 >> 3 does not carry).
+  auto frag16 = [&](const char* base, int row0) {
+    const int x = f16 ^ ((row0 >> 3) & 6);
+    const char* row = base + (row0 + r16) * TKB;
+    const i32x4_t lo = *(const i32x4_t*)(row + (((2 * g4) ^ x) * 16));
+    const i32x4_t hi = *(const i32x4_t*)(row + (((2 * g4 + 1) ^ x) * 16));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   };
-  float sxv[NJ], swv[NPB];
+  auto read_a = [&](Frag16& f, int s, int pb) {
+    f.a[pb] = frag16(smem + (s % NSTAGE) * STAGE_BYTES, arow[pb]);
+  };
+  auto read_b = [&](Frag16& f, int s, int jb) {
+    f.b[jb] = frag16(smem + (s % NSTAGE) * STAGE_BYTES + P_BYTES, 128 * wq + 16 * jb);
+  };
+  float sxv[NJ16], swv[NPB16];
   auto read_scales = [&](int s) {
     const char* st = smem + (s % NSTAGE) * STAGE_BYTES;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) sxv[j] = *(const float*)(st + SX_OFF + (128 * wq + 32 * j + r32) * 4);
+    for (int jb = 0; jb < NJ16; ++jb) sxv[jb] = *(const float*)(st + SX_OFF + (128 * wq + 16 * jb + r16) * 4);
 #pragma unroll
-    for (int pb = 0; pb < NPB; ++pb) {
-      const int lane = (EPI == EPI_SWIGLU) ? pb : 0;
+    for (int pb = 0; pb < NPB16; ++pb) {
+      const int lane = (EPI == EPI_SWIGLU) ? (pb >> 1) : 0;
       swv[pb] = *(const float*)(st + SW_OFF + w * 256 + lane * 4);
     }
   };
 
-  // ---- prologue: stages 0..2 in flight, stage 0 read --------------------------
+  // ---- prologue: stages 0..2 issued; stages 0 and 1 landed; stage 0 read ----
   issue(0);
   issue(1);
   issue(2);
-  wait_vm_barrier<2 * DMA_PER_STAGE>();
-  Frag8 f0, f1;
-  read_frag(f0, 0, 0);
-  read_frag(f1, 0, 1);
+  wait_vm_barrier<DMA_PER_STAGE>();
+  Frag16 f;
+#pragma unroll
+  for (int pb = 0; pb < NPB16; ++pb) read_a(f, 0, pb);
+#pragma unroll
+  for (int jb = 0; jb < NJ16; ++jb) read_b(f, 0, jb);
   read_scales(0);
 
   int s = 0;
@@ -223,66 +222,70 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
     const int4 ti = sload_int4(a.table + qt);
     const int row0 = ti.y, row1 = ti.z;
 
-    floatx16_t acc[NPB][NJ];
+    floatx4_t acc[NPB16][NJ16];
 #pragma unroll
-    for (int i = 0; i < NPB; ++i)
+    for (int i = 0; i < NPB16; ++i)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j)
+      for (int j = 0; j < NJ16; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+        for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
 
     for (int ks = 0; ks < ksteps; ++ks, ++s) {
-      // k = 128 partial sums of this stage, one per block
-      floatx16_t part[NPB][NJ];
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-#pragma unroll
-        for (int pb = 0; pb < NPB; ++pb) {
-          floatx16_t z = {};
-          z = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f0.a[pb], f0.b[j], z, 0, 0, 0, 127, 0, 127);
-          part[pb][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f1.a[pb], f1.b[j], z, 0, 0, 0, 127,
-                                                                         0, 127);
-        }
-      float sc[NPB][NJ];
-#pragma unroll
-      for (int pb = 0; pb < NPB; ++pb)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) sc[pb][j] = swv[pb] * sxv[j];
-      // Stage s + 1 has landed once only stage s + 2 may be in flight; every
-      // wave has read stage s (fragments and scales are in registers), so
-      // its buffer takes stage s + 3.
+      // Every wave has read stage s (fragments and scales are in registers)
+      // and stage s + 1 has landed (only s + 2 may be in flight): stage s's
+      // buffer takes stage s + 3, and stage s + 1 is read as registers free.
       wait_vm_barrier<DMA_PER_STAGE>();
       issue(s + NSTAGE);
-      read_frag(f0, s + 1, 0);
-      read_frag(f1, s + 1, 1);
+      float sw_cur[NPB16];
+#pragma unroll
+      for (int pb = 0; pb < NPB16; ++pb) sw_cur[pb] = swv[pb];
+      // The MFMAs of token block jb + 1 are issued before the scaled
+      // accumulation of block jb, so no FMA waits on an MFMA just issued.
+      floatx4_t part[2][NPB16];
+      auto mfma_block = [&](int jb, floatx4_t (&dst)[NPB16]) {
+#pragma unroll
+        for (int pb = 0; pb < NPB16; ++pb) {
+          floatx4_t z = {};
+          dst[pb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(f.a[pb], f.b[jb], z, 0, 0, 0, 127, 0, 127);
+        }
+      };
+      mfma_block(0, part[0]);
+#pragma unroll
+      for (int jb = 0; jb < NJ16; ++jb) {
+        if (jb + 1 < NJ16) mfma_block(jb + 1, part[(jb + 1) & 1]);
+        read_b(f, s + 1, jb);
+        const float sxj = sxv[jb];
+#pragma unroll
+        for (int pb = 0; pb < NPB16; ++pb) {
+          const float sc = sw_cur[pb] * sxj;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[pb][jb][v] += part[jb & 1][pb][v] * sc;
+        }
+      }
+#pragma unroll
+      for (int pb = 0; pb < NPB16; ++pb) read_a(f, s + 1, pb);
       read_scales(s + 1);
-#pragma unroll
-      for (int pb = 0; pb < NPB; ++pb)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[pb][j][v] += part[pb][j][v] * sc[pb][j];
     }
 
-    // ---- epilogue: acc[pb][j][4g + i] is (token row 128wq + 32j + r32,
-    //      weight row arow[pb] + 8g + 4 * half + i).
-    int er32 = r32;
-    asm volatile("" : "+v"(er32));
+    // ---- epilogue: acc[pb][jb][i] is (token row 128wq + 16jb + lane % 16,
+    //      weight row arow[pb] + 4 (lane / 16) + i).
+    int er16 = r16;
+    asm volatile("" : "+v"(er16));
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int gq = row0 + 128 * wq + 32 * j + er32;
+    for (int jb = 0; jb < NJ16; ++jb) {
+      const int gq = row0 + 128 * wq + 16 * jb + er16;
       const bool row_ok = gq < row1;
       if constexpr (EPI == EPI_SWIGLU) {
         const bool clamp = (a.limit == a.limit);
         const float L = a.limit;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int col = pt * 64 + 32 * wp + 8 * g + 4 * half;
+        for (int pb = 0; pb < 2; ++pb) {
+          const int col = pt * 64 + arow[pb] + 4 * g4;
           float av[4], gv[4], uv[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            gv[i] = round_bf16(acc[0][j][4 * g + i]);
-            uv[i] = round_bf16(acc[1][j][4 * g + i]);
+            gv[i] = round_bf16(acc[pb][jb][i]);
+            uv[i] = round_bf16(acc[pb + 2][jb][i]);
             float gc = gv[i], uc = uv[i];
             if (clamp) {
               gc = fminf(gc, L);
@@ -300,30 +303,25 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
             }
           }
         }
-        __builtin_amdgcn_sched_barrier(0);
       } else {
         float scl = 1.f;
         int orow_idx = gq;
         if constexpr (EPI == EPI_SCATTER) {
           const int* meta = (const int*)(smem + LDS_BYTES + (r % META_SLOTS) * META_BYTES);
-          const int qrow = 128 * wq + 32 * j + er32;
+          const int qrow = 128 * wq + 16 * jb + er16;
           if (a.dest) orow_idx = min(max(meta[qrow], 0), a.n_dest - 1);
           if (a.row_scale) scl = __int_as_float(meta[TQ + qrow]);
         }
         bf16_t* orow = a.out + (int64_t)orow_idx * a.ldo;
 #pragma unroll
-        for (int pb = 0; pb < NPB; ++pb) {
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int col = pt * TP + arow[pb] + 8 * g + 4 * half;
-            const floatx16_t& v = acc[pb][j];
-            const uint2 val = make_uint2(pack_bf16x2(v[4 * g] * scl, v[4 * g + 1] * scl),
-                                         pack_bf16x2(v[4 * g + 2] * scl, v[4 * g + 3] * scl));
-            if (row_ok) *(uint2*)(orow + col) = val;
-          }
-          __builtin_amdgcn_sched_barrier(0);
+        for (int pb = 0; pb < NPB16; ++pb) {
+          const int col = pt * TP + arow[pb] + 4 * g4;
+          const floatx4_t& v = acc[pb][jb];
+          const uint2 val = make_uint2(pack_bf16x2(v[0] * scl, v[1] * scl), pack_bf16x2(v[2] * scl, v[3] * scl));
+          if (row_ok) *(uint2*)(orow + col) = val;
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   wait_vm<0>();  // DMAs past the end have landed before the workgroup exits
