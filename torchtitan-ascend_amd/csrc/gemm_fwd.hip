@@ -7,14 +7,17 @@
 // epilogue, for the w2 down-projection with the routing-weight scale and the
 // un-permute scatter fused into the epilogue, and for the plain grouped GEMM.
 //
-// Tile: up to 256 token rows (Q) x 256 weight rows (P); k in stages of 64.
-//   * 4 waves, one per SIMD, in a 2 x 2 arrangement: wave (wq, wp) owns
-//     token rows 128wq.. and 128 weight rows, i.e. 4 x 4 accumulators of
-//     v_mfma_f32_32x32x16_bf16 (256 fp32 AGPRs per lane).  The MFMA A
-//     operand is the weight tile, B the token tile, so a lane holds 4
-//     consecutive output columns per register group.  SWIGLU: a wave's weight
-//     rows are 64 gate rows and the 64 matching up rows.
-//   * Two LDS stage buffers of 64 KB (32 KB weights + 32 KB tokens, rows of
+// Tile: up to 320 token rows (Q) x 256 weight rows (P); k in stages of 64.
+//   * 8 waves, two per SIMD, in a 2 x 4 arrangement: wave (wq, wp) owns 64
+//     weight rows and the tile's 32-row token blocks wq, wq + 2, ... (up to
+//     5 of them, 2 x 5 accumulators of v_mfma_f32_32x32x16_bf16, 160 fp32
+//     registers per lane).  The block count follows the tile's height (the
+//     k loop is instantiated per count), so a 256-row tile costs 256 rows of
+//     MFMA, LDS reads and token-row DMA, not 320.  The MFMA A operand is the
+//     weight tile, B the token tile, so a lane holds 4 consecutive output
+//     columns per register group.  SWIGLU: a wave's weight rows are 32 gate
+//     rows and the 32 matching up rows.
+//   * Two LDS stage buffers of 72 KB (32 KB weights + 40 KB tokens, rows of
 //     128 bytes = one full cache line per row and stage) filled by
 //     global_load_lds_dwordx4 (HBM/L2 -> LDS without VGPR staging).  A DMA
 //     instruction moves 8 whole rows; half-line rows (k stages of 32) cost
@@ -38,6 +41,8 @@
 //   :17-18, :31, :38  torch._grouped_mm(x, w.transpose(-2, -1), offs)
 //   :32-36            optional clamp with swiglu_limit
 //   :37               npu_swiglu: silu(gate) * up, gate = first H columns
+#include <type_traits>
+
 #include "common.h"
 #include "dma_asm.h"
 #include "gemm_common.h"
@@ -136,6 +141,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     }
   };
   int d_r = -1;  // tile round whose addresses are loaded
+  int d_qblk8 = 0;  // 8-row token blocks the MFMA reads: 4 * ceil(rows / 32)
   uint64_t d_pbase = 0, d_qbase = 0;
   uint32_t d_voff[DMA_PER_STAGE];
   auto dma_tile = [&](int r) {
@@ -145,6 +151,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     const int4 ti = sload_int4(a.table + qt);
     const int64_t ldp2 = a.ldp * 2;
     const int qmax = ti.z - ti.y - 1;
+    d_qblk8 = 4 * ((ti.z - ti.y + 31) >> 5);
 #pragma unroll
     for (int i = 0; i < DMA_P; ++i) {
       if constexpr (PT) {
@@ -216,8 +223,11 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     const uint32_t st = lds0 + (uint32_t)((s & 1) * STAGE_BYTES) + w * 1024;
 #pragma unroll
     for (int i = 0; i < DMA_P; ++i) dma16(d_voff[i], pb, st + i * (WAVES * 1024));
+    // Token rows past the tile's last 32-row block are never read: skip
+    // their DMA (wave-uniform: instruction i moves row block WAVES * i + w).
 #pragma unroll
-    for (int i = 0; i < DMA_Q; ++i) dma16(d_voff[DMA_P + i], qb, st + P_BYTES + i * (WAVES * 1024));
+    for (int i = 0; i < DMA_Q; ++i)
+      if (WAVES * i + w < d_qblk8) dma16(d_voff[DMA_P + i], qb, st + P_BYTES + i * (WAVES * 1024));
   };
 
   // ---- fragment geometry -------------------------------------------------------
@@ -251,7 +261,12 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
         trx[pb][par] = tr_row * (TP * 2) + ((tr_col & 4) << 1) +
                        ((((arow[pb] + tr_col) >> 3) ^ (4 * (bsw ^ (2 * par)))) << 4);
   }
-  auto read_frag = [&](Frag& f, int s, int kk) {
+  // Token block j of wave wq is the tile's 32-row block m = 2j + wq, so the
+  // chunk permutation term 4 * (m & 1) is 4 * wq for every block of a wave.
+  // njv (an integral constant) is the wave's block count in this tile.
+  auto read_frag = [&](Frag& f, int s, int kk, auto njv) {
+    constexpr int NJV = decltype(njv)::value;
+    if constexpr (NJV == 0) return;
     const char* st = smem + (s & 1) * STAGE_BYTES;
 #pragma unroll
     for (int pb = 0; pb < NPB; ++pb) {
@@ -269,36 +284,39 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
       f.a[pb] = *(const bf16x8_t*)(st + (arow[pb] + r32) * ROW_BYTES + pc * 16);
     }
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int m = NJ * wq + j;  // 32-row token block
-      const int pc = (2 * kk + half) ^ fa ^ (4 * (m & 1));
-      f.b[j] = *(const bf16x8_t*)(st + P_BYTES + (32 * m + r32) * ROW_BYTES + pc * 16);
+    for (int j = 0; j < NJV; ++j) {
+      const int pc = (2 * kk + half) ^ fa ^ (4 * wq);
+      f.b[j] = *(const bf16x8_t*)(st + P_BYTES + (64 * j + 32 * wq + r32) * ROW_BYTES + pc * 16);
     }
   };
 
-  // ---- prologue: stages 0 and 1 in flight, fragments of stage 0 / k16 0 read --
+  // ---- prologue: stages 0 and 1 in flight, stage 0 landed -----------------------
+  // (the token-row DMA count of a stage depends on its tile's height, so the
+  // wait is for everything issued)
   if constexpr (GATHER) {
     load_ids(0);
     wait_vm_barrier<0>();
   }
   issue(0);
   issue(1);
-  wait_vm_barrier<DMA_PER_STAGE>();
+  wait_vm_barrier<0>();
   Frag f0, f1;
-  read_frag(f0, 0, 0);
 
   int s = 0;
-  auto run_tile = [&](int r, int row0, int row1, int pt) {
-    floatx16_t acc[NPB][NJ];
+  auto run_tile = [&](auto njv, int r, int row0, int row1, int pt) {
+    constexpr int NJV = decltype(njv)::value;
+    read_frag(f0, s, 0, njv);
+    constexpr int NJA = NJV > 0 ? NJV : 1;
+    floatx16_t acc[NPB][NJA];
 #pragma unroll
     for (int i = 0; i < NPB; ++i)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j)
+      for (int j = 0; j < NJA; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
     auto mfma = [&](const Frag& f) {
 #pragma unroll
-      for (int j = 0; j < NJ; ++j)
+      for (int j = 0; j < NJV; ++j)
 #pragma unroll
         for (int pb = 0; pb < NPB; ++pb)
           acc[pb][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[pb], f.b[j], acc[pb][j], 0, 0, 0);
@@ -306,33 +324,34 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     // One stage: k16 steps 0..3, each computed from registers while the next
     // is read.  Before step 3 every wave has read all of stage s; the barrier
     // there also waits for stage s + 1 (the only stage in flight), and stage
-    // s + 2 is issued into stage s's buffer.
+    // s + 2 is issued into stage s's buffer.  Every wave runs the same
+    // barrier sequence whatever its block count.
     for (int ks = 0; ks + 1 < ksteps; ++ks, ++s) {
-      read_frag(f1, s, 1);
+      read_frag(f1, s, 1, njv);
       mfma(f0);
-      read_frag(f0, s, 2);
+      read_frag(f0, s, 2, njv);
       mfma(f1);
-      read_frag(f1, s, 3);
+      read_frag(f1, s, 3, njv);
       mfma(f0);
       wait_vm_barrier<0>();
       issue(s + 2);
-      read_frag(f0, s + 1, 0);
+      read_frag(f0, s + 1, 0, njv);
       mfma(f1);
     }
-    // Last stage of the tile: the next tile's first fragments are read after
-    // the epilogue (fewer live registers there).
-    read_frag(f1, s, 1);
+    // Last stage of the tile: the next tile's first fragments are read at
+    // the start of that tile, with its block count.
+    read_frag(f1, s, 1, njv);
     mfma(f0);
-    read_frag(f0, s, 2);
+    read_frag(f0, s, 2, njv);
     mfma(f1);
-    read_frag(f1, s, 3);
+    read_frag(f1, s, 3, njv);
     mfma(f0);
     wait_vm_barrier<0>();
     issue(s + 2);
     mfma(f1);
     ++s;
 
-    // ---- epilogue: acc[pb][j][4g + i] is (token row NJ*32wq + 32j + r32,
+    // ---- epilogue: acc[pb][j][4g + i] is (token row 64j + 32wq + r32,
     //      weight row arow[pb] + 8g + 4 * half + i).  Column validity is
     //      wave-uniform (H % 64 == 0 and N % 128 == 0 are required), row
     //      validity is per lane.  The scheduling barriers keep each block's
@@ -345,7 +364,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     // EPI_SWIGLU_BWD: saved pre-activation of token block jj
     auto load_h = [&](int jj, int pb, uint2 (&dst)[4][2]) {
       if constexpr (EPI == EPI_SWIGLU_BWD) {
-        const int gq = row0 + NJ * 32 * wq + 32 * jj + er32;
+        const int gq = row0 + 64 * jj + 32 * wq + er32;
         const int qrow = min(gq, row1 - 1);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -357,8 +376,8 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
       }
     };
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int gq = row0 + NJ * 32 * wq + 32 * j + er32;
+    for (int j = 0; j < NJV; ++j) {
+      const int gq = row0 + 64 * j + 32 * wq + er32;
       const bool row_ok = gq < row1;
       if constexpr (EPI == EPI_SWIGLU) {
         const bool clamp = (a.limit == a.limit);
@@ -451,7 +470,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
         int orow_idx = gq;
         if constexpr (EPI == EPI_SCATTER) {
           const int* meta = (const int*)(smem + LDS_BYTES + (r % 3) * META_BYTES);
-          const int qrow = NJ * 32 * wq + 32 * j + er32;
+          const int qrow = 64 * j + 32 * wq + er32;
           if (a.dest) orow_idx = min(max(meta[qrow], 0), a.n_dest - 1);
           if (a.row_scale) sc = __int_as_float(meta[TQ + qrow]);
         }
@@ -472,7 +491,6 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
         }
       }
     }
-    read_frag(f0, s, 0);  // first k16 step of the next stage (a valid buffer past the end)
   };
 
   for (int r = 0; r < nmy; ++r) {
@@ -480,7 +498,17 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     const int qt = tile / a.np_tiles;
     const int pt = tile - qt * a.np_tiles;
     const int4 ti = sload_int4(a.table + qt);
-    run_tile(r, ti.y, ti.z, pt);
+    // 32-row blocks of the tile (at most TQ / 32), interleaved over the two
+    // token-row waves: wave wq takes blocks wq, wq + 2, ...
+    const int nj = min((((ti.z - ti.y + 31) >> 5) + 1 - wq) >> 1, NJ);
+    switch (nj) {
+      case 5: run_tile(std::integral_constant<int, 5>{}, r, ti.y, ti.z, pt); break;
+      case 4: run_tile(std::integral_constant<int, 4>{}, r, ti.y, ti.z, pt); break;
+      case 3: run_tile(std::integral_constant<int, 3>{}, r, ti.y, ti.z, pt); break;
+      case 2: run_tile(std::integral_constant<int, 2>{}, r, ti.y, ti.z, pt); break;
+      case 1: run_tile(std::integral_constant<int, 1>{}, r, ti.y, ti.z, pt); break;
+      default: run_tile(std::integral_constant<int, 0>{}, r, ti.y, ti.z, pt); break;
+    }
   }
   wait_vm<0>();  // DMAs past the end have landed before the workgroup exits
 }
