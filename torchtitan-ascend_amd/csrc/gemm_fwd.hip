@@ -478,13 +478,29 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
 #pragma unroll
         for (int pb = 0; pb < NPB; ++pb) {
           if (pt * TP + arow[pb] < a.n_p) {
+            const floatx16_t& v = acc[pb][j];
+            uint32_t pk[4][2];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-              const int col = pt * TP + arow[pb] + 8 * g + 4 * half;
-              const floatx16_t& v = acc[pb][j];
-              const uint2 val = make_uint2(pack_bf16x2(v[4 * g] * sc, v[4 * g + 1] * sc),
-                                           pack_bf16x2(v[4 * g + 2] * sc, v[4 * g + 3] * sc));
-              if (row_ok) *(uint2*)(orow + col) = val;
+              pk[g][0] = pack_bf16x2(v[4 * g] * sc, v[4 * g + 1] * sc);
+              pk[g][1] = pack_bf16x2(v[4 * g + 2] * sc, v[4 * g + 3] * sc);
+            }
+            // Lanes l and l ^ 32 hold the same output row, half h holding
+            // columns 8g + 4h .. + 3 of group g.  Swapping one group each
+            // way leaves lane half h with columns 16c + 8h .. + 7 (c = 0, 1),
+            // so every store is 16 bytes and 32 contiguous bytes per row.
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+              uint32_t keep[2], recv[2];
+#pragma unroll
+              for (int d = 0; d < 2; ++d) {
+                keep[d] = half ? pk[2 * c + 1][d] : pk[2 * c][d];
+                recv[d] = (uint32_t)__shfl_xor((int)(half ? pk[2 * c][d] : pk[2 * c + 1][d]), 32, 64);
+              }
+              const u32x4_t val = half ? u32x4_t{recv[0], recv[1], keep[0], keep[1]}
+                                       : u32x4_t{keep[0], keep[1], recv[0], recv[1]};
+              const int col = pt * TP + arow[pb] + 16 * c + 8 * half;
+              if (row_ok) *(u32x4_t*)(orow + col) = val;
             }
           }
           __builtin_amdgcn_sched_barrier(0);
