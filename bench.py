@@ -2,8 +2,8 @@
 
 Default workload (Qwen3-30B-A3B shape, MoE layer
 forward, bf16): T=8192 tokens, D=2048, H=768, E=128 experts, top-8 softmax
-router with renormalised weights.  One step = router (gate GEMM as upstream
-runs it, then the HIP top-k) -> route (histogram + stable sort) -> permute
+router with renormalised weights.  One step = router (the fused gate GEMM +
+fp32 softmax + top-k + renorm kernel) -> route (histogram + stable sort) -> permute
 -> grouped GEMM w13 + SwiGLU -> grouped GEMM w2 + score + un-permute ->
 K-way sum, on inputs already resident in HBM.
 
@@ -113,8 +113,8 @@ def main():
     def router():
         if zipf_idx is not None:
             return zipf_scores, zipf_idx
-        logits = torch.matmul(x, w_router.t())  # upstream router gate (nn.Linear, bf16)
-        return ops.router_topk(logits, K, cfg["router"], cfg["norm"])
+        # gate nn.Linear (bf16) + fp32 score + top-k + renorm, one kernel
+        return ops.router_fused(x, w_router, K, cfg["router"], cfg["norm"])
 
     def timed_router(ev):
         if ev is None:

@@ -28,6 +28,8 @@ PINNED = {
     "permute / unpermute": "round trip unpermute(permute(x)) == x; torch index_select/index_add golden",
     "group_labels": "torch arange.repeat.repeat_interleave golden (npu_permute.py:68-72)",
     "router_topk": "torch softmax/sigmoid + topk golden on tie-free inputs; explicit tie cases",
+    "router_logits": "torch F.linear (fp32) rounded to bf16 golden; exact bf16 values (a missing rounding or a "
+                     "transposed weight fails it)",
     "experts_forward": "torch._grouped_mm golden; per-expert index_add loop and dense einsum forms",
     "moe_forward": "per-token brute loop of model.py:703-735 form",
     "moe_backward": "torch autograd of a torch fp32 restatement (golden); central finite differences",
@@ -166,6 +168,14 @@ def regroup_permute(routed_input: np.ndarray, counts_group: np.ndarray, ep_size:
 # Router top-k (UPSTREAM TokenChoiceTopKRouter; closed form in the reference
 # at models/qwen3_5/model.py:757-765)
 # ---------------------------------------------------------------------------
+def router_logits(x: np.ndarray, w_router: np.ndarray) -> np.ndarray:
+    """Router gate logits F.linear(x, weight) in bf16 (models/qwen3_5/model.py:757;
+    UPSTREAM TokenChoiceTopKRouter.gate is a bias-free nn.Linear): the bf16
+    inputs accumulated in float64, rounded once to bf16 (via fp32)."""
+    z = np.asarray(x, np.float64) @ np.asarray(w_router, np.float64).T
+    return bf16_round(z.astype(np.float32))
+
+
 def router_topk(logits: np.ndarray, top_k: int, score_func: str = "softmax", route_norm: bool = False,
                 route_scale: float = 1.0, expert_bias: np.ndarray | None = None, norm_eps: float = 1e-20):
     """Scores in fp32 (softmax over experts or sigmoid); pick the top_k by

@@ -119,6 +119,16 @@ def router_cases():
                   indices_bias=ib.numpy())
 
 
+def router_gate_case():
+    """F.linear of the router gate (models/qwen3_5/model.py:757), bf16 output."""
+    g = torch.Generator().manual_seed(7)
+    T, D, E = 48, 128, 40
+    x = _bf16(torch.randn(T, D, generator=g))
+    w = _bf16(torch.randn(E, D, generator=g) * 0.02)
+    logits = _bf16(F.linear(x.float(), w.float()))
+    _save("gate_linear", x=x.float().numpy(), w=w.float().numpy(), logits=logits.float().numpy())
+
+
 def experts_cases():
     """The reference's op sequence (npu_gmm.py:29-38) on CPU torch, bf16."""
     g = torch.Generator().manual_seed(3)
@@ -260,6 +270,7 @@ if __name__ == "__main__":
     routing_cases()
     permute_cases()
     router_cases()
+    router_gate_case()
     experts_cases()
     layer_cases()
     bf16_cases()

@@ -226,3 +226,59 @@ def test_router_ties(ops):
     announce("router ties")
     _, i = ops.router_topk(f32_dev(logits), 3, "sigmoid")
     np.testing.assert_array_equal(i.cpu().numpy(), [[1, 2, 4], [0, 1, 2]])
+
+
+def _bf16_ulp(v):
+    e = np.floor(np.log2(np.maximum(np.abs(v), 1e-30)))
+    return np.exp2(e - 7)
+
+
+@pytest.mark.parametrize("T,D,E,K,func,norm,bias", [
+    (1000, 2048, 128, 8, "softmax", True, False),   # Qwen3-30B-A3B router shape
+    (2048, 256, 8, 1, "sigmoid", False, False),     # Llama4-debugmodel
+    (300, 512, 16, 1, "sigmoid", False, False),     # Llama4-Scout expert count
+    (257, 384, 256, 8, "sigmoid", True, True),      # DeepSeek-V3 count, expert bias
+    (33, 128, 60, 4, "softmax", False, False),      # ragged token tile, E not a block multiple
+])
+def test_router_fused_vs_oracle(ops, T, D, E, K, func, norm, bias):
+    """Fused gate GEMM + top-k: the bf16 logits match the oracle's F.linear to
+    one bf16 step, and the selection on the kernel's own logits is the
+    oracle's, bit for bit (scores to fp32 rounding)."""
+    rng = np.random.default_rng(T + E)
+    x = rand_bf16(rng, (T, D))
+    w = rand_bf16(rng, (E, D), 0.02)
+    eb = (rng.standard_normal(E) * 0.05).astype(np.float32) if bias else None
+    announce(f"router_fused T={T} D={D} E={E} K={K} {func} norm={norm} bias={bias}")
+    s, i, lg = ops.router_fused(bf16_dev(x), bf16_dev(w), K, func, norm, route_scale=1.25,
+                                expert_bias=None if eb is None else f32_dev(eb), return_logits=True)
+    lg = to_np(lg)
+    ref_lg = O.router_logits(x, w)
+    d = np.abs(lg - ref_lg)
+    # one bf16 step of the result plus the fp32 dot-product error bound
+    # gamma_D * sum |x||w| (summation order differs from the oracle's)
+    gamma = D * 2.0 ** -24 / (1 - D * 2.0 ** -24)
+    bound = _bf16_ulp(ref_lg) * 1.01 + gamma * (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T)
+    assert np.all(d <= bound)
+    assert (d > 0).mean() < 0.02
+    rs, ri = O.router_topk(lg, K, func, norm, route_scale=1.25, expert_bias=eb)
+    np.testing.assert_array_equal(to_np(i), ri)
+    np.testing.assert_allclose(to_np(s), rs, rtol=2e-6, atol=1e-7)
+    # without the logits output: same result
+    s2, i2 = ops.router_fused(bf16_dev(x), bf16_dev(w), K, func, norm, route_scale=1.25,
+                              expert_bias=None if eb is None else f32_dev(eb))
+    np.testing.assert_array_equal(to_np(i2), ri)
+    np.testing.assert_array_equal(to_np(s2), to_np(s))
+
+
+def test_router_fused_matches_two_stage(ops):
+    """On the Qwen3-30B-A3B shape the fused router picks what the two-stage
+    path (gate GEMM, then ttamd_router_topk) picks on the same logits."""
+    rng = np.random.default_rng(5)
+    T, D, E, K = 8192, 2048, 128, 8
+    x = bf16_dev(rand_bf16(rng, (T, D)))
+    w = bf16_dev(rand_bf16(rng, (E, D), 0.02))
+    announce("router_fused vs two-stage, C2 shape")
+    s, i, lg = ops.router_fused(x, w, K, "softmax", True, return_logits=True)
+    s2, i2 = ops.router_topk(lg.float(), K, "softmax", True)
+    assert torch.equal(i, i2)
+    torch.testing.assert_close(s, s2, rtol=2e-6, atol=1e-7)

@@ -132,6 +132,27 @@ def test_router_topk_matches_torch(name):
     np.testing.assert_allclose(s, g["scores_bias"], rtol=1e-6, atol=1e-7)
 
 
+def _bf16_ulp(v):
+    """Spacing of bf16 values at |v| (8 significant bits)."""
+    e = np.floor(np.log2(np.maximum(np.abs(v), 1e-30)))
+    return np.exp2(e - 7)
+
+
+def test_router_logits_match_torch_linear():
+    """F.linear in fp32 rounded to bf16 (torch golden): exact bf16 values up to
+    one bf16 step on a few entries (summation order); a missing bf16
+    rounding or a transposed weight fails it."""
+    g = load_golden("gate_linear")
+    z = O.router_logits(g["x"], g["w"])
+    d = np.abs(z - g["logits"])
+    assert np.all(d <= _bf16_ulp(g["logits"]) * 1.01)
+    assert (d > 0).mean() < 0.01
+    unrounded = (np.asarray(g["x"], np.float64) @ np.asarray(g["w"], np.float64).T).astype(np.float32)
+    assert (unrounded != g["logits"]).mean() > 0.5
+    with pytest.raises(ValueError):
+        O.router_logits(g["x"], g["w"].T)
+
+
 def test_router_ties_prefer_lower_expert():
     logits = np.array([[1.0, 3.0, 3.0, 0.0, 3.0], [2.0, 2.0, 2.0, 2.0, 2.0]], np.float32)
     _, i = O.router_topk(logits, 3, "sigmoid")

@@ -33,6 +33,9 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   return (uint32_t)__builtin_bit_cast(uint16_t, b);
 }
 
+// fp32 -> bf16 (round to nearest even) -> fp32.
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
 // Pack two floats into one dword of two bf16 (lo in bits 0..15).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);

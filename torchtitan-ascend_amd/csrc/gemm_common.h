@@ -15,8 +15,6 @@ enum Epi {
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
 
-__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
-
 // Token-row tiles: table[i] = {expert, first row, end row, 0}, at most
 // kFwdTileRows rows (bf16 forward and dgrad) or kFp8TileRows (fp8).  The
 // workspace is sized for tiles of kTileRows rows, fewer rows than either,

@@ -122,6 +122,52 @@ def router_topk(
     return scores, idx
 
 
+def router_fused(
+    x: torch.Tensor,
+    w_router: torch.Tensor,
+    top_k: int,
+    score_func: str = "softmax",
+    route_norm: bool = False,
+    route_scale: float = 1.0,
+    expert_bias: torch.Tensor | None = None,
+    norm_eps: float = 1e-20,
+    return_logits: bool = False,
+):
+    """Gate GEMM + score + top-k in one kernel (upstream TokenChoiceTopKRouter;
+    in-reference closed form torchtitanturbo/models/qwen3_5/model.py:752-766).
+
+    x bf16 [T, D] (any leading shape), w_router bf16 [E, D].  The logits are
+    the bf16 F.linear output; selection as `router_topk` on them.  Returns
+    (top_scores fp32 [T, K], selected_experts_indices int64 [T, K]) and, with
+    return_logits, the bf16 logits [T, E] as a third element.
+    """
+    dev = _gpu("x", x)
+    x = _want("x", x.reshape(-1, x.shape[-1]), _BF16)
+    w_router = _want("w_router", w_router, _BF16)
+    T, D = x.shape
+    E, D2 = w_router.shape
+    if D2 != D:
+        raise ValueError(f"w_router must be [E, {D}], got {tuple(w_router.shape)}")
+    funcs = {"softmax": 0, "sigmoid": 1}
+    if score_func not in funcs:
+        raise ValueError(f"score_func must be one of {sorted(funcs)}")
+    if expert_bias is not None:
+        _same_device(dev, expert_bias=expert_bias)
+        expert_bias = expert_bias.float().contiguous()
+        if expert_bias.shape != (E,):
+            raise ValueError("expert_bias must be [E]")
+    scores = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+    idx = torch.empty(T, top_k, dtype=torch.int64, device=dev)
+    logits = torch.empty(T, E, dtype=_BF16, device=dev) if return_logits else None
+    _lib.call(
+        "ttamd_router_fused", _p(x), _p(w_router), _p(expert_bias), T, E, D, top_k, funcs[score_func],
+        int(bool(route_norm)), float(norm_eps), float(route_scale), _p(scores), _p(idx), _p(logits), _stream(dev),
+    )
+    if return_logits:
+        return scores, idx, logits
+    return scores, idx
+
+
 def route(
     selected_experts_indices: torch.Tensor,
     num_experts: int,
