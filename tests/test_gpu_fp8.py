@@ -51,6 +51,43 @@ def test_quantize_rows_bit_exact(ops, R, K):
     np.testing.assert_array_equal(s_t.cpu().numpy(), scale.T)
 
 
+def test_quantize_rows_every_bf16_pattern(ops):
+    """Every bf16 value of magnitude below 448 (both signs, subnormals, zero)
+    through the row quantiser with a block scale of exactly 1 (each
+    128-channel block also holds 448): the device e4m3 cast must equal the
+    oracle's round-to-nearest-even cast on all of them."""
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    vals = (bits << 16).view(np.float32)
+    vals = vals[np.isfinite(vals) & (np.abs(vals) < 448.0)]
+    nblk = (vals.size + 126) // 127
+    x = np.zeros((nblk, 128), np.float32)
+    x[:, 0] = 448.0
+    flat = x[:, 1:].reshape(-1)
+    flat[: vals.size] = vals
+    x[:, 1:] = flat.reshape(nblk, 127)
+    x = x.reshape(-1, 1024) if nblk % 8 == 0 else np.pad(x, ((0, 8 - nblk % 8), (0, 0))).reshape(-1, 1024)
+    x[:, ::128] = 448.0
+    announce(f"quantize_fp8_rows every bf16 pattern ({vals.size} values)")
+    q, s_t = ops.quantize_fp8_rows(bf16_dev(x))
+    ref_bits, ref_scale = O.quantize_fp8_rows(x)
+    assert np.all(ref_scale == 1.0)
+    np.testing.assert_array_equal(s_t.cpu().numpy(), ref_scale.T)
+    np.testing.assert_array_equal(q.cpu().numpy(), ref_bits)
+
+
+def test_quantize_rows_many_near_ties(ops):
+    """29 M normal values with scales that are not powers of two: about a
+    hundred quotients land within two fp32 ulps of an e4m3 halfway point,
+    where only the exact division decides the rounding."""
+    rng = np.random.default_rng(11)
+    x = rand_bf16(rng, (4096, 7168))
+    announce("quantize_fp8_rows 4096 x 7168 near-tie sweep")
+    q, s_t = ops.quantize_fp8_rows(bf16_dev(x))
+    bits, scale = O.quantize_fp8_rows(x)
+    np.testing.assert_array_equal(s_t.cpu().numpy(), scale.T)
+    np.testing.assert_array_equal(q.cpu().numpy(), bits)
+
+
 @pytest.mark.parametrize("with_scale", [False, True])
 def test_quantize_rows_gather_bit_exact(ops, with_scale):
     """Fused permute: routed row j = x[src_index[j] // K] (times the routing

@@ -32,14 +32,33 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
   return sign | (e << 3) | ((r >> 20) & 7u);
 }
 
+// Can the e4m3 rounding of q depend on bits an approximate quotient gets
+// wrong?  In the normal e4m3 range the cast keeps 3 mantissa bits, so only a
+// quotient within a few fp32 ulps of the halfway pattern (low 20 bits =
+// 0x80000) can round differently; 16 ulps each side is a wide margin for
+// f * rcp(s) (two roundings plus rcp's 1 ulp).  Below 2^-6 (e4m3 subnormals,
+// zero) the quotient is always taken exactly.
+__device__ __forceinline__ bool e4m3_tie_risk(float q) {
+  const uint32_t u = __float_as_uint(q) & 0x7fffffffu;
+  return u < 0x3c800000u || ((u & 0xfffffu) - 0x7fff0u) <= 0x20u;
+}
+
 // ---------------------------------------------------------------------------
-// Rows: a workgroup of 4 waves quantises 16 rows (4 per wave).  A wave walks
-// its row 512 channels at a time: lane l holds 8 consecutive channels, 16
-// lanes form one 128-channel block.  Scales go through LDS so that each
-// k-block's 16 row scales leave as one 64-byte store.
+// Rows: a workgroup of 4 waves quantises 16 rows (4 per wave).  Lane l holds
+// 8 consecutive channels of every 512-channel step (16 lanes form one
+// 128-channel block).  All of a row's loads are issued before any of its
+// arithmetic (up to kMaxSteps x 16 bytes per lane), so a wave keeps its whole
+// row in flight instead of one 1 KB step at a time.  Scales go through LDS
+// so that each k-block's 16 row scales leave as one 64-byte store.
+// The quotient v / s is f * rcp(s), replaced by the exact division wherever
+// e4m3_tie_risk says the last bits could matter (a wave-uniform branch,
+// taken for a few percent of steps), and v_cvt_pk_fp8_f32 (round to nearest
+// even, OCP e4m3) packs the bytes: the result is the IEEE quotient's cast,
+// bit for bit, at a fraction of the VALU work of a division per element.
 // ---------------------------------------------------------------------------
 constexpr int kQRows = 16;
 constexpr int kMaxKBlocks = 64;  // K <= 8192
+constexpr int kMaxSteps = kMaxKBlocks / 4;  // 512-channel steps per row
 
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint4* __restrict__ in,
                                                             const int* __restrict__ src_index,
@@ -61,15 +80,19 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint4* __restr
     const float mul = row_mul ? row_mul[row] : 1.f;
     const uint4* irow = in + (int64_t)src * kv;
     uint2* orow = q_out + (int64_t)row * kv;
-    for (int c = l; c < ((kv + 63) & ~63); c += 64) {
+    uint4 v[kMaxSteps];
+#pragma unroll
+    for (int it = 0; it < kMaxSteps; ++it) {
+      const int c = l + 64 * it;
+      v[it] = (c < kv) ? irow[c] : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int it = 0; it < kMaxSteps; ++it) {
+      if (64 * it >= kv) break;  // wave-uniform
+      const int c = l + 64 * it;
       const bool ok = c < kv;
       float f[8];
-      if (ok) {
-        unpack8(irow[c], f);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) f[i] = 0.f;
-      }
+      unpack8(v[it], f);  // zero past the row end
       if (row_mul) {
         // the dispatched row is materialised in bf16 after the score multiply
 #pragma unroll
@@ -81,12 +104,25 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint4* __restr
 #pragma unroll
       for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
       const float s = m / 448.0f;
-      uint32_t b[8];
+      const float rs = (s > 0.f) ? __builtin_amdgcn_rcpf(s) : 0.f;
+      float q[8];
+      bool risk = false;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) b[i] = (s > 0.f) ? f32_to_e4m3(f[i] / s) : 0u;
+      for (int i = 0; i < 8; ++i) {
+        q[i] = f[i] * rs;
+        risk |= e4m3_tie_risk(q[i]);
+      }
+      if (__builtin_amdgcn_ballot_w64(risk && s > 0.f)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (s > 0.f && e4m3_tie_risk(q[i])) q[i] = f[i] / s;
+      }
+      int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
+      int hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], hi, true);
       if (ok) {
-        orow[c] = make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24),
-                             b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
+        orow[c] = make_uint2((uint32_t)lo, (uint32_t)hi);
         if ((l & 15) == 0) sc[c >> 4][rr] = s;
       }
     }
