@@ -131,25 +131,37 @@ def main():
         w13q, s13 = ops.quantize_fp8_blocks(w13)
         w2q, s2 = ops.quantize_fp8_blocks(w2)
 
+    shared = cfg.get("shared", False)
+    if shared:
+        # the always-on shared expert: the same SwiGLU FFN on every token
+        sw13 = (torch.randn(2 * H, D, device=dev) * 0.02).to(torch.bfloat16)
+        sw2 = (torch.randn(D, H, device=dev) * 0.02).to(torch.bfloat16)
+
     def step_forward(ev=None):
         scores, idx = timed_router(ev)
         if fp8:
             return F.moe_experts_forward_fp8(x, scores, idx, w13q, s13, w2q, s2, E, cfg["score_before"],
                                              stage_events=ev)
-        return F.moe_experts_forward(x, scores, idx, w13, w2, E, cfg["score_before"], stage_events=ev)
+        out = F.moe_experts_forward(x, scores, idx, w13, w2, E, cfg["score_before"], stage_events=ev)
+        if shared:
+            # no autograd here: one fused pass, the shared w2 GEMM adds into out
+            pair = ev.setdefault("shared_expert", (torch.cuda.Event(enable_timing=True),
+                                                   torch.cuda.Event(enable_timing=True))) if ev is not None else None
+            if pair:
+                pair[0].record()
+            out = F.shared_expert_combine(out, x, sw13, sw2)
+            if pair:
+                pair[1].record()
+        return out
 
     if cfg["backward"]:
         w13p = w13.clone().requires_grad_(True)
         w2p = w2.clone().requires_grad_(True)
         dout = torch.randn(T, D, device=dev).to(torch.bfloat16)
         xg = x.clone().requires_grad_(True)
-        shared = cfg.get("shared", False)
         if shared:
-            # the always-on shared expert: the same SwiGLU FFN on every token,
-            # run as a one-expert grouped GEMM
-            sw13 = (torch.randn(1, 2 * H, D, device=dev) * 0.02).to(torch.bfloat16).requires_grad_(True)
-            sw2 = (torch.randn(1, D, H, device=dev) * 0.02).to(torch.bfloat16).requires_grad_(True)
-            all_tokens = torch.full((1,), T, dtype=torch.int32, device=dev)
+            sw13.requires_grad_(True)
+            sw2.requires_grad_(True)
 
         def step(ev=None):
             # a training step starts from cleared gradients (zero_grad(set_to_none=True))
@@ -159,7 +171,7 @@ def main():
             out = F.moe_experts_forward(xg, scores, idx, w13p, w2p, E, cfg["score_before"])
             if shared:
                 sw13.grad = sw2.grad = None
-                out = out + F.run_experts_grouped_mm(sw13, sw2, xg, all_tokens)
+                out = F.shared_expert_combine(out, xg, sw13, sw2)
             out.backward(dout)
             return out
     else:

@@ -298,6 +298,30 @@ int ttamd_moe_sum_topk(const void* in, int64_t num_tokens, int64_t hidden,
                        int topk, void* out, void* stream);
 
 /*
+ * Shared expert fused into the combine: out[t] += g(t) * FFN(x[t]), where
+ *   FFN(x) = (silu(gate) * up) @ w2_shared^T with [gate | up] = x @ w13_shared^T
+ *            (gate rows 0..H-1, up rows H..2H-1; optional clamp as
+ *            ttamd_grouped_mm_swiglu), one bf16 FeedForward;
+ *   g(t)   = sigmoid(gate_logits[t]) when gate_logits (fp32 [T]) is given,
+ *            else 1.
+ * Replaces the shared-expert tail of the reference MoE block,
+ * torchtitanturbo/models/qwen3_5/model.py:796-809 (shared_expert FeedForward,
+ * sigmoid(shared_expert_gate(x)) * shared, expert_output + shared), and
+ * UPSTREAM Llama4's ungated `out + shared_experts(x)`.  out bf16 [T, D]
+ * holds the combined routed output on entry and the sum on return;
+ * a_scratch bf16 [T, H] is caller-owned scratch (the SwiGLU output).
+ * x bf16 [T, D]; w13_shared [2H, D]; w2_shared [D, H]; D % 128 == 0,
+ * H % 64 == 0; workspace: ttamd_gemm_workspace_bytes(T, 1).
+ * swiglu_limit: <= 0 or NaN = no clamp.
+ */
+int ttamd_shared_expert_add(const void* x, int64_t num_tokens, int64_t dim,
+                            int64_t hidden, const void* w13_shared,
+                            const void* w2_shared, const float* gate_logits,
+                            float swiglu_limit, void* a_scratch, void* out,
+                            void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/*
  * Grouped dgrad: dx[m, k] = sum_n dy[m, n] * w[e(m), n, k]  (bf16 out).
  * Backward of ttamd_grouped_mm w.r.t. x; w [E, N, K] with K contiguous.
  * N % 64 == 0, K % 128 == 0.

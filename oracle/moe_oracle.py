@@ -32,6 +32,9 @@ PINNED = {
                      "transposed weight fails it)",
     "experts_forward": "torch._grouped_mm golden; per-expert index_add loop and dense einsum forms",
     "moe_forward": "per-token brute loop of model.py:703-735 form",
+    "shared_expert_add": "torch bf16 golden of the reference block's op sequence (FeedForward w1/w3/w2 Linear, "
+                         "sigmoid(shared_expert_gate), expert_output + shared, model.py:794-809); a dropped gate "
+                         "fails it",
     "moe_backward": "torch autograd of a torch fp32 restatement (golden); central finite differences",
     "bf16_round": "torch .to(bfloat16) on random and special values",
     "f32_to_e4m3_bits / e4m3_bits_to_f32": "torch .to(float8_e4m3fn) on every bf16 bit pattern, ties and edge "
@@ -253,6 +256,22 @@ def experts_forward(x: np.ndarray, w13: np.ndarray, w2: np.ndarray, counts: np.n
     if round_intermediates:
         y = bf16_round(y)
     return y, h, a
+
+
+def shared_expert_add(routed_out: np.ndarray, x: np.ndarray, w13s: np.ndarray, w2s: np.ndarray,
+                      gate_logits: np.ndarray | None = None, swiglu_limit: float | None = None) -> np.ndarray:
+    """Shared expert added to the combined routed output
+    (models/qwen3_5/model.py:794-809; UPSTREAM Llama4 MoE: out + shared_experts(x)):
+      y     = FeedForward(x): silu(x w1^T) * (x w3^T), then w2, each Linear
+              output in bf16 (w1 / w3 are the gate / up halves of w13s [2H, D]);
+      g     = sigmoid(gate_logits) in bf16 (Linear(D, 1) output, :804-807), or 1;
+      out   = bf16(routed_out + bf16(g * y))                         (:808)."""
+    T = x.shape[0]
+    y, _, _ = experts_forward(x, w13s[None], w2s[None], np.array([T]), swiglu_limit)
+    if gate_logits is not None:
+        g = bf16_round((1.0 / (1.0 + np.exp(-np.asarray(gate_logits, np.float64)))).astype(np.float32))
+        y = bf16_round(g.reshape(T, 1) * y)
+    return bf16_round(np.asarray(routed_out, np.float32) + y)
 
 
 def moe_forward(x: np.ndarray, top_scores: np.ndarray, idx: np.ndarray, w13: np.ndarray, w2: np.ndarray,

@@ -158,6 +158,27 @@ def experts_cases():
         )
 
 
+def shared_expert_case():
+    """The reference block's shared-expert sequence (models/qwen3_5/model.py:794-809)
+    on CPU torch in bf16: FeedForward (w1, w3, w2 Linear), sigmoid of the
+    Linear(D, 1) gate, then expert_output + shared_expert_output."""
+    g = torch.Generator().manual_seed(8)
+    T, D, H = 24, 64, 32
+    x = _bf16(torch.randn(T, D, generator=g))
+    w1 = _bf16(torch.randn(H, D, generator=g) * 0.1)
+    w3 = _bf16(torch.randn(H, D, generator=g) * 0.1)
+    w2 = _bf16(torch.randn(D, H, generator=g) * 0.1)
+    wg = _bf16(torch.randn(1, D, generator=g) * 0.1)
+    routed = _bf16(torch.randn(T, D, generator=g))
+    shared = F.linear(F.silu(F.linear(x, w1)) * F.linear(x, w3), w2)
+    gate_logits = F.linear(x, wg)
+    gated = torch.sigmoid(gate_logits) * shared
+    _save("shared_expert_gated", x=x.float().numpy(), w13=torch.cat([w1, w3]).float().numpy(),
+          w2=w2.float().numpy(), gate_logits=gate_logits.float().numpy().reshape(T),
+          routed=routed.float().numpy(), out=(routed + gated).float().numpy(),
+          out_ungated=(routed + shared).float().numpy())
+
+
 def layer_cases():
     """Whole layer fwd + bwd through torch autograd on an fp32 restatement
     (dispatch gather, per-expert F.linear, combine with index_add_ in the
@@ -271,6 +292,7 @@ if __name__ == "__main__":
     permute_cases()
     router_cases()
     router_gate_case()
+    shared_expert_case()
     experts_cases()
     layer_cases()
     bf16_cases()

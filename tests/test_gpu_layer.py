@@ -3,6 +3,7 @@ combine) against the CPU oracle, forward and backward, including the
 BASELINE configs at full size (checked on sampled tokens)."""
 from __future__ import annotations
 
+import importlib
 import zlib
 
 import numpy as np
@@ -149,3 +150,51 @@ def test_c4_deepseek_shard_full_size_sampled(pkg, ops):
     announce("C4 full size")
     err = _full_size_sampled(pkg, ops, 32768, 7168, 2048, 32, 1, "sigmoid", False, False, n_sample=24, labels=labels)
     assert err < TOL
+
+
+@pytest.mark.parametrize("T,D,H,gated,limit", [(300, 256, 128, True, None), (1000, 512, 192, False, None),
+                                              (77, 128, 64, True, 0.4)])
+def test_shared_expert_add_vs_oracle(pkg, ops, T, D, H, gated, limit):
+    """Shared expert fused into the combine (the shared w2 GEMM adds into the
+    routed output in its epilogue) against the oracle's block tail."""
+    rng = np.random.default_rng(T + D)
+    x = rand_bf16(rng, (T, D))
+    w13 = rand_bf16(rng, (2 * H, D), 0.08)
+    w2 = rand_bf16(rng, (D, H), 0.08)
+    routed = rand_bf16(rng, (T, D))
+    gl = (rng.standard_normal(T) * 2).astype(np.float32) if gated else None
+    announce(f"shared_expert_add T={T} D={D} H={H} gated={gated} limit={limit}")
+    out = bf16_dev(routed)
+    ops.shared_expert_add(out, bf16_dev(x), bf16_dev(w13), bf16_dev(w2),
+                          None if gl is None else torch.from_numpy(gl).to(DEV), limit)
+    ref = O.shared_expert_add(routed, x, w13, w2, gl, limit)
+    assert O.max_rel_err(to_np(out), ref) < 2e-2
+    # the functional form (no autograd: the fused pass) gives the same bits
+    F = importlib.import_module("torchtitan-ascend_amd.functional")
+    with torch.no_grad():
+        out2 = F.shared_expert_combine(bf16_dev(routed), bf16_dev(x), bf16_dev(w13), bf16_dev(w2),
+                                       None if gl is None else torch.from_numpy(gl).to(DEV), limit)
+    assert torch.equal(out2, out)
+
+
+def test_shared_expert_combine_autograd(pkg, ops):
+    """With autograd the shared expert runs as a one-expert ExpertsFn and the
+    gate in torch; forward matches the fused pass and gradients reach x,
+    both shared weights, the gate logits and the routed output."""
+    rng = np.random.default_rng(3)
+    T, D, H = 200, 256, 128
+    F = importlib.import_module("torchtitan-ascend_amd.functional")
+    x = bf16_dev(rand_bf16(rng, (T, D))).requires_grad_(True)
+    w13 = bf16_dev(rand_bf16(rng, (2 * H, D), 0.08)).requires_grad_(True)
+    w2 = bf16_dev(rand_bf16(rng, (D, H), 0.08)).requires_grad_(True)
+    routed = bf16_dev(rand_bf16(rng, (T, D))).requires_grad_(True)
+    gl = torch.from_numpy(rng.standard_normal(T).astype(np.float32)).to(DEV).requires_grad_(True)
+    announce("shared_expert_combine autograd")
+    out = F.shared_expert_combine(routed, x, w13, w2, gl)
+    with torch.no_grad():
+        fused = F.shared_expert_combine(routed, x, w13, w2, gl)
+    assert O.max_rel_err(to_np(out.detach()), to_np(fused)) < 2e-2
+    out.float().square().sum().backward()
+    for name, t in (("x", x), ("w13", w13), ("w2", w2), ("gate_logits", gl), ("routed", routed)):
+        assert t.grad is not None and torch.isfinite(t.grad.float()).all(), name
+        assert t.grad.float().abs().sum() > 0, name

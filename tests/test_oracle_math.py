@@ -153,6 +153,17 @@ def test_router_logits_match_torch_linear():
         O.router_logits(g["x"], g["w"].T)
 
 
+def test_shared_expert_add_matches_torch_block():
+    """The reference block's shared-expert tail in torch bf16 (golden):
+    gated and ungated within one bf16 step; dropping the gate fails it."""
+    g = load_golden("shared_expert_gated")
+    out = O.shared_expert_add(g["routed"], g["x"], g["w13"], g["w2"], g["gate_logits"])
+    assert O.max_rel_err(out, g["out"]) < 1e-2
+    out0 = O.shared_expert_add(g["routed"], g["x"], g["w13"], g["w2"], None)
+    assert O.max_rel_err(out0, g["out_ungated"]) < 1e-2
+    assert O.max_rel_err(out0, g["out"]) > 5e-2
+
+
 def test_router_ties_prefer_lower_expert():
     logits = np.array([[1.0, 3.0, 3.0, 0.0, 3.0], [2.0, 2.0, 2.0, 2.0, 2.0]], np.float32)
     _, i = O.router_topk(logits, 3, "sigmoid")

@@ -80,6 +80,11 @@ SIGNATURES: dict[str, tuple] = {
          _c_void_p, _sz, _c_void_p],
     ),
     "ttamd_moe_sum_topk": (_i32, [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p]),
+    "ttamd_shared_expert_add": (
+        _i32,
+        [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _f32, _c_void_p, _c_void_p, _c_void_p, _sz,
+         _c_void_p],
+    ),
     "ttamd_grouped_mm_dgrad": (
         _i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i64, _i64, _c_void_p, _c_void_p, _sz, _c_void_p]
     ),

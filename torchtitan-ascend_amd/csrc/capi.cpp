@@ -441,6 +441,30 @@ int ttamd_grouped_mm_unpermute(const void* a, const void* w2, const int32_t* off
                    fn);
 }
 
+int ttamd_shared_expert_add(const void* x, int64_t num_tokens, int64_t dim, int64_t hidden,
+                            const void* w13_shared, const void* w2_shared, const float* gate_logits,
+                            float swiglu_limit, void* a_scratch, void* out, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  const char* fn = "ttamd_shared_expert_add";
+  REQUIRE(num_tokens >= 0 && num_tokens <= (1 << 28), "%s: num_tokens out of range", fn);
+  TRY(check_dim(fn, "dim", dim, 128));
+  TRY(check_dim(fn, "hidden", hidden, 64));
+  REQUIRE(w13_shared && aligned16(w13_shared) && w2_shared && aligned16(w2_shared),
+          "%s: shared weights must be non-null and 16-byte aligned", fn);
+  TRY(check_rows(fn, "x", x, num_tokens, dim));
+  TRY(check_rows(fn, "a_scratch", a_scratch, num_tokens, hidden));
+  TRY(check_rows(fn, "out", out, num_tokens, dim));
+  if (num_tokens > 0)
+    REQUIRE(a_scratch != out && a_scratch != x, "%s: a_scratch must not alias x or out", fn);
+  TRY(check_ws(fn, workspace, workspace_bytes, ttamd::gemm_workspace_bytes(num_tokens, 1)));
+  if (num_tokens == 0) return TTAMD_OK;
+  const float lim = (swiglu_limit > 0.f) ? swiglu_limit : NAN;
+  return check_hip(ttamd::launch_shared_expert_add(x, (int)num_tokens, (int)dim, (int)hidden, w13_shared,
+                                                   w2_shared, gate_logits, lim, a_scratch, out, workspace,
+                                                   (hipStream_t)stream),
+                   fn);
+}
+
 int ttamd_grouped_mm_dgrad(const void* dy, const void* w, const int32_t* offs, int64_t num_rows,
                            int num_experts, int64_t n, int64_t k, void* dx, void* workspace,
                            size_t workspace_bytes, void* stream) {

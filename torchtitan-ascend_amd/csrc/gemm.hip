@@ -20,7 +20,8 @@ namespace ttamd {
 // device from the inclusive group offsets, so no count reaches the host.
 // An expert's rows are split into the fewest tiles of at most max_rows rows,
 // of equal height rounded up to 32 rows (540 rows at max_rows = 320 give
-// 2 tiles of 288 rather than 320 + 220).
+// 2 tiles of 288 rather than 320 + 220).  A null offs means one expert
+// (E == 1) with all M rows.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void tile_map_kernel(const int* __restrict__ offs, int E,
                                                         int M, int max_tiles, int max_rows,
@@ -30,8 +31,9 @@ __global__ __launch_bounds__(1024) void tile_map_kernel(const int* __restrict__ 
   const int tid = threadIdx.x;
   int r0 = 0, r1 = 0, nt = 0, h = max_rows;
   if (tid < E) {
-    const int a = (tid == 0) ? 0 : offs[tid - 1];
-    const int b = offs[tid];
+    // offs == nullptr: one expert owning all M rows
+    const int a = (tid == 0 || !offs) ? 0 : offs[tid - 1];
+    const int b = offs ? offs[tid] : M;
     r0 = min(max(a, 0), M);
     r1 = min(max(b, r0), M);
     const int c = r1 - r0;
@@ -196,6 +198,20 @@ static hipError_t dgrad(int epi, DgradGemm g, const int* offs, int E, int M, voi
   g.table = tt.table;
   g.n_qtiles = tt.count;
   return launch_dgrad_gemm(epi, g, stream);
+}
+
+hipError_t launch_shared_expert_add(const void* x, int T, int D, int H, const void* w13s, const void* w2s,
+                                   const float* gate_logits, float limit, void* a_scratch, void* out,
+                                   void* ws, hipStream_t stream) {
+  // one expert with all T rows: a = swiglu(x w13s^T), then out += g(t) * (a w2s^T)
+  FwdGemm g1 = {};
+  g1.act = x; g1.w = w13s; g1.kred = D; g1.n = H; g1.out = a_scratch; g1.limit = limit;
+  hipError_t err = fwd(EPI_SWIGLU, g1, nullptr, 1, T, ws, stream);
+  if (err != hipSuccess) return err;
+  FwdGemm g2 = {};
+  g2.act = a_scratch; g2.w = w2s; g2.kred = H; g2.n = D; g2.out = out; g2.n_dest = T;
+  g2.row_scale = gate_logits; g2.scale_sigmoid = 1; g2.accumulate = 1;
+  return fwd(EPI_SCATTER, g2, nullptr, 1, T, ws, stream);
 }
 
 hipError_t launch_grouped_mm_dgrad(const void* dy, const void* w, const int* offs, int M, int E,

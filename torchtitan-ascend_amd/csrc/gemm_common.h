@@ -58,6 +58,8 @@ struct FwdGemm {
   const float* row_scale;
   const int* dest;
   int n_dest;
+  int accumulate;     // EPI_SCATTER: out[dest] = bf16(out[dest] + v) instead of bf16(v)
+  int scale_sigmoid;  // EPI_SCATTER: the row scale is sigmoid(row_scale[j])
 };
 
 // Kernel arguments of the forward GEMMs (gemm_fwd.hip, gemm_ring.hip).
@@ -89,6 +91,8 @@ struct FwdArgs {
   const float* row_scale;
   const int* dest;
   int n_dest;
+  int accumulate;
+  int scale_sigmoid;
 };
 
 // Grouped dgrad through the forward kernel's reduction-major weight mode:

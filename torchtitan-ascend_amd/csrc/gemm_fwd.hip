@@ -472,7 +472,10 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
           const int* meta = (const int*)(smem + LDS_BYTES + (r % 3) * META_BYTES);
           const int qrow = 64 * j + 32 * wq + er32;
           if (a.dest) orow_idx = min(max(meta[qrow], 0), a.n_dest - 1);
-          if (a.row_scale) sc = __int_as_float(meta[TQ + qrow]);
+          if (a.row_scale) {
+            sc = __int_as_float(meta[TQ + qrow]);
+            if (a.scale_sigmoid) sc = 1.f / (1.f + __expf(-sc));
+          }
         }
         bf16_t* orow = a.out + (int64_t)orow_idx * a.ldo;
 #pragma unroll
@@ -500,7 +503,20 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
               const u32x4_t val = half ? u32x4_t{recv[0], recv[1], keep[0], keep[1]}
                                        : u32x4_t{keep[0], keep[1], recv[0], recv[1]};
               const int col = pt * TP + arow[pb] + 16 * c + 8 * half;
-              if (row_ok) *(u32x4_t*)(orow + col) = val;
+              if (row_ok) {
+                if (a.accumulate) {
+                  // add to the row already there (bf16 + bf16, one rounding)
+                  const u32x4_t prev = *(const u32x4_t*)(orow + col);
+                  u32x4_t sum;
+#pragma unroll
+                  for (int d = 0; d < 4; ++d)
+                    sum[d] = pack_bf16x2(bf16_to_f32(val[d] & 0xffffu) + bf16_to_f32(prev[d] & 0xffffu),
+                                         bf16_to_f32(val[d] >> 16) + bf16_to_f32(prev[d] >> 16));
+                  *(u32x4_t*)(orow + col) = sum;
+                } else {
+                  *(u32x4_t*)(orow + col) = val;
+                }
+              }
             }
           }
           __builtin_amdgcn_sched_barrier(0);
@@ -590,6 +606,8 @@ hipError_t launch_fwd_gemm(int epi, const FwdGemm& g, hipStream_t stream) {
   a.row_scale = g.row_scale;
   a.dest = g.dest;
   a.n_dest = g.n_dest;
+  a.accumulate = g.accumulate;
+  a.scale_sigmoid = g.scale_sigmoid;
   if (epi == EPI_SCATTER) return launch_fwd<EPI_SCATTER>(a, stream);
   return launch_fwd<EPI_STORE>(a, stream);
 }

@@ -51,6 +51,9 @@ hipError_t launch_grouped_mm_unpermute(const void* act, const void* w2, const in
                                        int E, int D, int H, const float* row_scale,
                                        const int* dest, int n_dest, void* out, void* ws,
                                        hipStream_t stream);
+hipError_t launch_shared_expert_add(const void* x, int T, int D, int H, const void* w13s, const void* w2s,
+                                   const float* gate_logits, float limit, void* a_scratch, void* out,
+                                   void* ws, hipStream_t stream);
 hipError_t launch_grouped_mm_dgrad(const void* dy, const void* w, const int* offs, int M, int E,
                                    int N, int K, void* dx, void* ws, hipStream_t stream);
 hipError_t launch_grouped_mm_dgrad_swiglu(const void* dy, const void* w2, const void* h,

@@ -155,6 +155,38 @@ def run_experts_grouped_mm(
     return y.type_as(x)
 
 
+def shared_expert_combine(
+    routed_out: torch.Tensor,
+    x: torch.Tensor,
+    w13_shared: torch.Tensor,
+    w2_shared: torch.Tensor,
+    gate_logits: torch.Tensor | None = None,
+    swiglu_limit: float | None = None,
+) -> torch.Tensor:
+    """routed_out + g * shared_expert(x), g = sigmoid(gate_logits) or 1
+    (torchtitanturbo/models/qwen3_5/model.py:796-809; UPSTREAM Llama4 adds the
+    ungated shared expert).  x [T, D]; w13_shared [2H, D]; w2_shared [D, H].
+
+    Without autograd this is one fused pass (ttamd_shared_expert_add: the
+    shared w2 GEMM adds into the routed output in its epilogue).  With
+    autograd it runs the shared FFN as a one-expert ExpertsFn and composes
+    the gate and the sum in torch, so every input gets its gradient."""
+    needs_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (routed_out, x, w13_shared, w2_shared, gate_logits))
+    if not needs_grad:
+        out = routed_out.to(_BF16).contiguous().clone()
+        ops.shared_expert_add(out, x.to(_BF16), w13_shared, w2_shared,
+                              None if gate_logits is None else gate_logits.float(), swiglu_limit)
+        return out
+    T = x.shape[0]
+    all_rows = torch.full((1,), T, dtype=torch.int32, device=x.device)
+    y = ExpertsFn.apply(x.to(_BF16).contiguous(), w13_shared.unsqueeze(0), w2_shared.unsqueeze(0), all_rows,
+                        swiglu_limit)
+    if gate_logits is not None:
+        y = torch.sigmoid(gate_logits.to(y.dtype)).reshape(T, 1) * y
+    return routed_out + y
+
+
 def moe_experts_forward(
     x: torch.Tensor,
     top_scores: torch.Tensor,

@@ -583,6 +583,42 @@ def grouped_mm_wgrad(
 _U8 = torch.uint8
 
 
+def shared_expert_add(
+    out: torch.Tensor,
+    x: torch.Tensor,
+    w13_shared: torch.Tensor,
+    w2_shared: torch.Tensor,
+    gate_logits: torch.Tensor | None = None,
+    swiglu_limit: float | None = None,
+) -> torch.Tensor:
+    """In place: out[t] += g(t) * FFN(x[t]) with FFN the shared SwiGLU expert
+    (w13_shared [2H, D] gate-then-up, w2_shared [D, H]) and g = sigmoid(gate_logits)
+    or 1 (torchtitanturbo/models/qwen3_5/model.py:796-809).  Returns out."""
+    dev = _gpu("x", x)
+    x = _want("x", x, _BF16)
+    w13_shared = _want("w13_shared", w13_shared, _BF16)
+    w2_shared = _want("w2_shared", w2_shared, _BF16)
+    if out.dtype != _BF16 or not out.is_contiguous():
+        raise TypeError("out must be a contiguous bf16 tensor (it is updated in place)")
+    T, D = x.shape
+    H2, D2 = w13_shared.shape
+    H = H2 // 2
+    if D2 != D or H2 % 2 or tuple(w2_shared.shape) != (D, H) or tuple(out.shape) != (T, D):
+        raise ValueError(f"shapes: x {tuple(x.shape)}, w13_shared {tuple(w13_shared.shape)}, "
+                         f"w2_shared {tuple(w2_shared.shape)}, out {tuple(out.shape)}")
+    _same_device(dev, out=out, w13_shared=w13_shared, w2_shared=w2_shared)
+    if gate_logits is not None:
+        gate_logits = _want("gate_logits", gate_logits.reshape(T), torch.float32)
+    a = torch.empty(T, H, dtype=_BF16, device=dev)
+    ws = _gemm_ws(T, 1, dev)
+    _lib.call(
+        "ttamd_shared_expert_add", _p(x), T, D, H, _p(w13_shared), _p(w2_shared), _p(gate_logits),
+        _limit(swiglu_limit), _p(a), _p(out),
+        _p(ws), ws.numel(), _stream(dev),
+    )
+    return out
+
+
 def quantize_fp8_rows(
     x: torch.Tensor,
     src_index: torch.Tensor | None = None,
