@@ -13,6 +13,7 @@ side effects: nothing is patched, nothing is loaded until an op runs.
 from .functional import HIPMoeTokenUnpermute, moe_experts_forward, run_experts_grouped_mm
 from .grouped_experts import HipGroupedExperts, HipGroupedExpertsConverter
 from .protocol import HAVE_TORCHTITAN
+from . import state_dict
 from .token_dispatcher import HipDispatchMetadata, HipTokenDispatcher, HipTokenDispatcherConverter
 
 __all__ = [
@@ -25,4 +26,5 @@ __all__ = [
     "HipTokenDispatcherConverter",
     "moe_experts_forward",
     "run_experts_grouped_mm",
+    "state_dict",
 ]

@@ -21,6 +21,7 @@ from torch import nn
 
 from .functional import ExpertsFn, moe_experts_forward, run_experts_grouped_mm
 from .protocol import GroupedExperts, Module, ModelConfigConverter
+from .state_dict import upstream_to_fused
 from .token_dispatcher import HipTokenDispatcher
 
 
@@ -35,6 +36,14 @@ def _local(p: torch.Tensor) -> tuple[torch.Tensor, bool]:
         is_tp = any(isinstance(pl, Shard) and pl.dim == 2 for pl in p.placements)
         return p.to_local(), is_tp
     return p, False
+
+
+def _load_upstream_w1_w3(state_dict, prefix, *args, **kwargs):
+    """load_state_dict pre-hook: {prefix}w1 + {prefix}w3 -> {prefix}w13."""
+    if prefix + "w1" in state_dict and prefix + "w13" not in state_dict:
+        fused = upstream_to_fused({k: state_dict[k] for k in (prefix + "w1", prefix + "w3")}, prefix)
+        del state_dict[prefix + "w1"], state_dict[prefix + "w3"]
+        state_dict[prefix + "w13"] = fused[prefix + "w13"]
 
 
 class HipGroupedExperts(Module):
@@ -56,6 +65,8 @@ class HipGroupedExperts(Module):
         self.w13 = nn.Parameter(torch.empty(E, 2 * H, D))
         self.w2 = nn.Parameter(torch.empty(E, D, H))
         self.token_dispatcher = config.token_dispatcher.build()
+        # checkpoints of upstream GroupedExperts (w1 / w3 [E, H, D]) load as w13
+        self._register_load_state_dict_pre_hook(_load_upstream_w1_w3)
 
     def _weights(self):
         w2, tp2 = _local(self.w2)
