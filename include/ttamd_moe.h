@@ -73,7 +73,7 @@ int ttamd_router_topk(const float* logits, const float* expert_bias,
                       int64_t* top_indices, void* stream);
 
 /*
- * Fused router: gate GEMM + score + top-k (+ renorm) in one kernel.
+ * Router forward: gate GEMM + score + top-k (+ renorm).
  * Replaces upstream TokenChoiceTopKRouter.forward (gate nn.Linear in bf16,
  * fp32 score, topk, renorm); in-reference closed form
  * torchtitanturbo/models/qwen3_5/model.py:752-766 (F.linear :757, softmax
@@ -81,15 +81,19 @@ int ttamd_router_topk(const float* logits, const float* expert_bias,
  *   logits[t, e] = bf16(sum_d x[t, d] * w_router[e, d])  (fp32 accumulate)
  *   then exactly as ttamd_router_topk on those logits.
  * x bf16 [T, D], w_router bf16 [E, D]; D % 64 == 0; 1 <= K <= min(16, E);
- * E <= 256; E * D * 2 < 2^31.  logits_out (nullable) receives the bf16
- * logits [T, E] (needs E % 4 == 0).  Outputs as ttamd_router_topk.
+ * E <= 256.  logits_out (nullable) receives the bf16 logits [T, E].
+ * Outputs as ttamd_router_topk.  workspace: ttamd_router_workspace_bytes
+ * (fp32 partial logits of the split gate GEMM).
  */
+size_t ttamd_router_workspace_bytes(int64_t num_tokens, int num_experts,
+                                    int64_t dim);
 int ttamd_router_fused(const void* x, const void* w_router,
                        const float* expert_bias, int64_t num_tokens,
                        int num_experts, int64_t dim, int topk, int score_func,
                        int renorm, float renorm_eps, float route_scale,
                        float* top_scores, int64_t* top_indices,
-                       void* logits_out, void* stream);
+                       void* logits_out, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /* Bytes of device workspace ttamd_moe_route / ttamd_moe_token_permute need. */
 size_t ttamd_route_workspace_bytes(int64_t num_flat, int num_experts);

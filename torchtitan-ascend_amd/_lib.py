@@ -28,10 +28,11 @@ SIGNATURES: dict[str, tuple] = {
         _i32,
         [_c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _i32, _f32, _f32, _c_void_p, _c_void_p, _c_void_p],
     ),
+    "ttamd_router_workspace_bytes": (_sz, [_i64, _i32, _i64]),
     "ttamd_router_fused": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i64, _i32, _i32, _i32, _f32, _f32, _c_void_p, _c_void_p,
-         _c_void_p, _c_void_p],
+         _c_void_p, _c_void_p, _sz, _c_void_p],
     ),
     "ttamd_route_workspace_bytes": (_sz, [_i64, _i32]),
     "ttamd_moe_route": (

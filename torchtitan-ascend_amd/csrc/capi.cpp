@@ -116,12 +116,18 @@ int ttamd_router_topk(const float* logits, const float* expert_bias, int64_t num
                    fn);
 }
 
+size_t ttamd_router_workspace_bytes(int64_t num_tokens, int num_experts, int64_t dim) {
+  if (num_tokens <= 0 || num_experts < 1 || dim < 64) return 0;
+  return ttamd::router_workspace_bytes(num_tokens, num_experts, dim);
+}
+
 int ttamd_router_fused(const void* x, const void* w_router, const float* expert_bias,
                        int64_t num_tokens, int num_experts, int64_t dim, int topk, int score_func,
                        int renorm, float renorm_eps, float route_scale, float* top_scores,
-                       int64_t* top_indices, void* logits_out, void* stream) {
+                       int64_t* top_indices, void* logits_out, void* workspace, size_t workspace_bytes,
+                       void* stream) {
   const char* fn = "ttamd_router_fused";
-  REQUIRE(num_tokens >= 0 && num_tokens <= kI32Max, "%s: num_tokens out of range", fn);
+  REQUIRE(num_tokens >= 0 && num_tokens <= (1 << 24), "%s: num_tokens out of range", fn);
   REQUIRE(num_experts >= 1 && num_experts <= 256, "%s: num_experts must be in [1, 256]", fn);
   REQUIRE(topk >= 1 && topk <= 16 && topk <= num_experts, "%s: topk must be in [1, min(16, E)]",
           fn);
@@ -129,17 +135,15 @@ int ttamd_router_fused(const void* x, const void* w_router, const float* expert_
           "%s: unknown score_func %d", fn, score_func);
   REQUIRE(dim >= 64 && dim % 64 == 0 && dim <= (1 << 20), "%s: dim must be a positive multiple of 64",
           fn);
-  REQUIRE((int64_t)num_experts * dim * 2 < kI32Max, "%s: router weight too large", fn);
-  REQUIRE(logits_out == nullptr || num_experts % 4 == 0,
-          "%s: logits_out needs num_experts %% 4 == 0", fn);
+  REQUIRE((int64_t)num_experts * dim * 2 < kI32Max && 128 * dim * 2 < kI32Max,
+          "%s: router weight too large", fn);
   if (num_tokens == 0) return TTAMD_OK;
   REQUIRE(x && w_router && top_scores && top_indices, "%s: null pointer argument", fn);
   REQUIRE(aligned16(x) && aligned16(w_router), "%s: x and w_router must be 16-byte aligned", fn);
-  REQUIRE(logits_out == nullptr || ((uintptr_t)logits_out & 7u) == 0,
-          "%s: logits_out must be 8-byte aligned", fn);
+  TRY(check_ws(fn, workspace, workspace_bytes, ttamd::router_workspace_bytes(num_tokens, num_experts, dim)));
   return check_hip(ttamd::launch_router_fused(x, w_router, expert_bias, (int)num_tokens, num_experts,
                                               (int)dim, topk, score_func, renorm, renorm_eps,
-                                              route_scale, top_scores, top_indices, logits_out,
+                                              route_scale, top_scores, top_indices, logits_out, workspace,
                                               (hipStream_t)stream),
                    fn);
 }

@@ -31,9 +31,11 @@ hipError_t launch_router_topk(const float* logits, const float* bias, int T, int
                               float* top_scores, int64_t* top_idx, hipStream_t stream);
 
 // router.hip
+size_t router_workspace_bytes(int64_t T, int E, int64_t D);
 hipError_t launch_router_fused(const void* x, const void* w, const float* bias, int T, int E, int D, int K,
                                int score_func, int renorm, float renorm_eps, float route_scale,
-                               float* top_scores, int64_t* top_idx, void* logits, hipStream_t stream);
+                               float* top_scores, int64_t* top_idx, void* logits, void* ws,
+                               hipStream_t stream);
 
 // gemm.hip
 int gemm_max_qtiles(int M, int E);

@@ -1,5 +1,4 @@
-// Fused MoE router on MI355X (gfx950): gate GEMM + score + top-k + renorm in
-// one kernel, so the router logits never round-trip through HBM.
+// MoE router on MI355X (gfx950): gate GEMM + score + top-k + renorm.
 //
 //   logits[t, e] = bf16(sum_d x[t, d] * w[e, d])      F.linear in bf16
 //   s[t, e]      = softmax_e(logits[t]) in fp32       or sigmoid(logits)
@@ -12,16 +11,23 @@
 // torchtitanturbo/models/qwen3_5/model.py:752-766 (F.linear :757, softmax in
 // fp32 :758, topk :759-761, renorm :762-764).
 //
-// Layout: one workgroup (4 waves) per 32 tokens.  k runs in stages of 64:
-// each stage holds the 32 token rows and the (32 * EB) expert rows as whole
-// 128-byte lines in LDS, filled by global_load_lds_dwordx4 (NST buffers,
-// NST - 1 stages in flight: the stream is latency-bound, so the pipeline
-// fills the LDS).  Wave w owns expert blocks w, w + 4, ... and runs
-// v_mfma_f32_32x32x16_bf16 with the expert block as A and the tokens as B,
-// so lane l ends with 16 logits of token l % 32.  The logits go through LDS
-// to the top-k, where 16 lanes own one token (4 tokens per wave at a time).
+// Two kernels.  The gate GEMM is memory-bound and every CU can only pull its
+// operands at the rate its in-flight line requests allow, so what matters
+// is the bytes each CU moves.  Giving each workgroup all experts for a few
+// tokens would make every CU stream the whole router weight; instead
+//   * router_gemm_kernel<EB>: a workgroup (4 waves) takes 128 tokens and one
+//     slice of D, streams those token rows and the slice of every expert
+//     row through LDS (whole 128-byte lines, global_load_lds_dwordx4, NST
+//     stage buffers) into v_mfma_f32_32x32x16_bf16 (wave w: token block w,
+//     all expert blocks), and writes fp32 partial logits [S][T][E];
+//   * router_topk_partials_kernel: sums the S partial logits of a token in a
+//     fixed order, rounds to bf16 (the Linear's output dtype) and runs the
+//     score + top-k with 16 lanes per token (4 tokens per wave).
+// The split count S is chosen so that the first kernel has about one
+// workgroup per CU.
 #include "common.h"
 #include "dma_asm.h"
+#include "gemm_common.h"
 #include "kernels.h"
 
 namespace ttamd {
@@ -29,57 +35,51 @@ namespace {
 
 using namespace dma;
 
-constexpr int RT = 32;      // tokens per workgroup
-constexpr int RWAVES = 4;
+constexpr int RT = 128;     // tokens per workgroup of the gate GEMM
+constexpr int RWAVES = 4;   // one 32-token block per wave
 constexpr int RTHREADS = 64 * RWAVES;
 constexpr int RTK = 64;     // k per stage: 128-byte rows
+constexpr int kRouterMaxE = 256;
+constexpr int kRouterMaxSplits = 4;  // slices of D (partial logits per token and expert)
 
-// Stage buffers: as many as fit next to the logits block (at most 8), so
-// that up to 7 stages stream in at once.
+// Stage buffers of the gate GEMM: as many as fit (at most 6).
 template <int EB>
 constexpr int router_nst() {
   constexpr int stage = (RT + 32 * EB) * 128;
-  constexpr int lg = RT * (32 * EB + 1) * 4;
-  constexpr int n = (160 * 1024 - lg) / stage;
-  return n > 8 ? 8 : n;
+  constexpr int n = (160 * 1024) / stage;
+  return n > 6 ? 6 : n;
 }
 
-struct RouterArgs {
-  const bf16_t* x;     // [T, D]
-  const bf16_t* w;     // [E, D]
-  const float* bias;   // [E] or null
-  int T, E, D, K;
-  int score_func;      // 0 softmax, 1 sigmoid
-  int renorm;
-  float eps, route_scale;
-  float* scores;       // [T, K]
-  int64_t* idx;        // [T, K]
-  bf16_t* logits;      // [T, E] or null
+struct RouterGemmArgs {
+  const bf16_t* x;  // [T, D]
+  const bf16_t* w;  // [E, D]
+  int T, E, D;
+  int kstages;      // 64-wide k stages per split
+  float* part;      // [S][T][E] fp32
 };
 
 template <int EB>
-__global__ __launch_bounds__(RTHREADS) void router_fused_kernel(const RouterArgs a) {
-  constexpr int EP = 32 * EB;       // experts padded to whole MFMA blocks
-  constexpr int ROWS = RT + EP;     // stage rows: tokens, then experts
+__global__ __launch_bounds__(RTHREADS) void router_gemm_kernel(const RouterGemmArgs a) {
+  constexpr int EP = 32 * EB;
+  constexpr int ROWS = RT + EP;            // stage rows: tokens, then experts
   constexpr int STAGE = ROWS * 128;
-  constexpr int DPW = ROWS / 8 / RWAVES;  // DMA instructions per wave per stage (= 1 + EB)
-  constexpr int PL = EP / 16;       // top-k values per lane
-  constexpr int LGS = EP + 1;       // logits row stride in LDS (floats)
+  constexpr int DPW = ROWS / 8 / RWAVES;   // DMA instructions per wave per stage
+  constexpr int TPW = RT / 8 / RWAVES;     // of which token rows (= 4)
   constexpr int NST = router_nst<EB>();
-  static_assert(ROWS % (8 * RWAVES) == 0, "stage rows");
-  static_assert(NST >= 3 && (NST - 2) * DPW < 64, "pipeline depth");
+  static_assert(ROWS % (8 * RWAVES) == 0 && NST >= 3 && (NST - 2) * DPW < 64, "router geometry");
   extern __shared__ __attribute__((aligned(1024))) char smem[];
-  float* lg = (float*)(smem + NST * STAGE);
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63;
   const int t0 = blockIdx.x * RT;
-  const int nst = a.D / RTK;
+  const int split = blockIdx.y;
+  const int k0 = split * a.kstages;                    // first stage of this slice
+  const int nst = min(a.kstages, a.D / RTK - k0);      // stages of this slice
   const uint32_t lds0 = lds_addr(smem);
   const int64_t ld2 = (int64_t)a.D * 2;
 
-  // DMA geometry: instruction i of wave w moves row block rb = 4 i + w (rows
-  // 8 rb .. 8 rb + 7); instruction 0 carries token rows, the rest expert rows.
+  // Instruction i of wave w moves row block rb = 4 i + w (rows 8 rb ..
+  // 8 rb + 7): instructions 0..TPW-1 carry token rows, the rest expert rows.
   // LDS row r holds its logical 16-byte chunk c at physical chunk c ^ cswz(r).
   uint32_t voff[DPW];
 #pragma unroll
@@ -87,28 +87,28 @@ __global__ __launch_bounds__(RTHREADS) void router_fused_kernel(const RouterArgs
     const int rb = RWAVES * i + w;
     const int row = 8 * rb + (l >> 3);
     const int lchunk = (l & 7) ^ cswz(row);
-    const int src = (i == 0) ? min(row, a.T - 1 - t0) : min(row - RT, a.E - 1);
+    const int src = (i < TPW) ? min(row, a.T - 1 - t0) : min(row - RT, a.E - 1);
     voff[i] = (uint32_t)(src * ld2 + lchunk * 16);
   }
-  const uint64_t xbase = (uint64_t)(a.x + (int64_t)t0 * a.D);
-  const uint64_t wbase = (uint64_t)a.w;
+  const uint64_t xbase = (uint64_t)(a.x + (int64_t)t0 * a.D + (int64_t)k0 * RTK);
+  const uint64_t wbase = (uint64_t)(a.w + (int64_t)k0 * RTK);
   auto issue = [&](int s) {
     const int sc = min(s, nst - 1);  // past the end: re-load the last stage
     const uint32_t st = lds0 + (uint32_t)((s % NST) * STAGE) + w * 1024;
-    dma16(voff[0], xbase + (uint64_t)sc * 128, st);
 #pragma unroll
-    for (int i = 1; i < DPW; ++i) dma16(voff[i], wbase + (uint64_t)sc * 128, st + i * (RWAVES * 1024));
+    for (int i = 0; i < DPW; ++i)
+      dma16(voff[i], (i < TPW ? xbase : wbase) + (uint64_t)sc * 128, st + i * (RWAVES * 1024));
   };
 
-  constexpr int NEB = (EB + RWAVES - 1) / RWAVES;  // expert blocks per wave
-  floatx16_t acc[NEB];
+  floatx16_t acc[EB];
 #pragma unroll
-  for (int b = 0; b < NEB; ++b)
+  for (int b = 0; b < EB; ++b)
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[b][v] = 0.f;
 
   const int r32 = l & 31;
   const int half = l >> 5;
+  const int trow = 32 * w + r32;  // this lane's token row in the stage
 #pragma unroll
   for (int s = 0; s < NST - 1; ++s) issue(s);
   for (int s = 0; s < nst; ++s) {
@@ -118,172 +118,266 @@ __global__ __launch_bounds__(RTHREADS) void router_fused_kernel(const RouterArgs
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int c = 2 * kk + half;
-      const bf16x8_t bx = *(const bf16x8_t*)(st + r32 * 128 + ((c ^ cswz(r32)) << 4));
+      const bf16x8_t bx = *(const bf16x8_t*)(st + trow * 128 + ((c ^ cswz(trow)) << 4));
 #pragma unroll
-      for (int b = 0; b < NEB; ++b) {
-        const int eb = w + RWAVES * b;
-        if (eb < EB) {
-          const int row = RT + 32 * eb + r32;
-          const bf16x8_t aw = *(const bf16x8_t*)(st + row * 128 + ((c ^ cswz(row)) << 4));
-          acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aw, bx, acc[b], 0, 0, 0);
-        }
+      for (int b = 0; b < EB; ++b) {
+        const int row = RT + 32 * b + r32;
+        const bf16x8_t aw = *(const bf16x8_t*)(st + row * 128 + ((c ^ cswz(row)) << 4));
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aw, bx, acc[b], 0, 0, 0);
       }
     }
   }
   wait_vm<0>();
 
-  // ---- logits: lane l holds token r32, experts 32 eb + 8 g + 4 half + v ------
-  const int tok = t0 + r32;
+  // lane l holds token t0 + trow, experts 32 b + 8 g + 4 half + v
+  const int tok = t0 + trow;
+  if (tok < a.T) {
+    float* prow = a.part + ((int64_t)split * a.T + tok) * a.E;
 #pragma unroll
-  for (int b = 0; b < NEB; ++b) {
-    const int eb = w + RWAVES * b;
-    if (eb < EB) {
+    for (int b = 0; b < EB; ++b)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int e0 = 32 * eb + 8 * g + 4 * half;
-        float v[4];
+        const int e0 = 32 * b + 8 * g + 4 * half;
+        if ((a.E & 3) == 0 && e0 + 3 < a.E) {
+          *(floatx4_t*)(prow + e0) = floatx4_t{acc[b][4 * g], acc[b][4 * g + 1], acc[b][4 * g + 2], acc[b][4 * g + 3]};
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[i] = round_bf16(acc[b][4 * g + i]);
-          lg[r32 * LGS + e0 + i] = v[i];
-        }
-        if (a.logits && tok < a.T && e0 < a.E) {
-          // E % 4 == 0: the 4 experts are valid together
-          *(uint2*)(a.logits + (int64_t)tok * a.E + e0) =
-              make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+          for (int i = 0; i < 4; ++i)
+            if (e0 + i < a.E) prow[e0 + i] = acc[b][4 * g + i];
         }
       }
+  }
+}
+
+struct RouterTopkArgs {
+  const float* part;  // [S][T][E]
+  int S, T, E, K;
+  const float* bias;  // [E] or null
+  int score_func;     // 0 softmax, 1 sigmoid
+  int renorm;
+  float eps, route_scale;
+  float* scores;      // [T, K]
+  int64_t* idx;       // [T, K]
+  bf16_t* logits;     // [T, E] or null
+};
+
+// All-reduce over the 16 lanes of a DPP row in four pairwise steps: xor 1,
+// xor 2 (quad permutes), then the half-row and row mirrors.  Each step
+// combines a lane with one partner and the pairs are symmetric, so with a
+// commutative combine every lane ends with bit-identical results.
+constexpr int kDppXor1 = 0xb1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4e;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each 8
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within the row
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  return fmaxf(v, dpp_f<kDppMirror>(v));
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<kDppXor1>(v);
+  v += dpp_f<kDppXor2>(v);
+  v += dpp_f<kDppHalfMirror>(v);
+  return v + dpp_f<kDppMirror>(v);
+}
+
+// (selection value desc, expert id asc) winner, with its unbiased score.
+template <int CTRL>
+__device__ __forceinline__ void argmax_step(float& bv, int& bi, float& bs) {
+  const float ov = dpp_f<CTRL>(bv);
+  const int oi = dpp_i<CTRL>(bi);
+  const float os = dpp_f<CTRL>(bs);
+  if (ov > bv || (ov == bv && oi < bi)) {
+    bv = ov;
+    bi = oi;
+    bs = os;
+  }
+}
+
+// 16 lanes per token (lane i holds experts i + 16 m), 4 tokens per wave,
+// 16 tokens per workgroup.
+template <int PL>
+__global__ __launch_bounds__(256) void router_topk_partials_kernel(const RouterTopkArgs a) {
+  const int l = threadIdx.x & 63;
+  const int gi = l & 15;
+  const int t = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const bool valid = t < a.T;
+  const int tt = valid ? t : a.T - 1;
+  float sc[PL], sel[PL];
+  // every partial first (one batch of independent loads), then the sums in
+  // split order
+  float pv[kRouterMaxSplits][PL];
+#pragma unroll
+  for (int s = 0; s < kRouterMaxSplits; ++s)
+#pragma unroll
+    for (int m = 0; m < PL; ++m) {
+      const int e = gi + 16 * m;
+      pv[s][m] = (s < a.S && e < a.E) ? a.part[((int64_t)s * a.T + tt) * a.E + e] : 0.f;
+    }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int m = 0; m < PL; ++m) {
+    const int e = gi + 16 * m;
+    float z = -INFINITY;
+    if (e < a.E) {
+      z = pv[0][m];
+#pragma unroll
+      for (int s = 1; s < kRouterMaxSplits; ++s)
+        if (s < a.S) z += pv[s][m];
+      z = round_bf16(z);
+      if (a.logits && valid) a.logits[(int64_t)t * a.E + e] = (bf16_t)f32_to_bf16(z);
+    }
+    sc[m] = z;
+    mx = fmaxf(mx, z);
+  }
+  if (a.score_func == 0) {
+    mx = row16_max(mx);
+    float sum = 0.f;
+#pragma unroll
+    for (int m = 0; m < PL; ++m) {
+      const int e = gi + 16 * m;
+      sc[m] = (e < a.E) ? expf(sc[m] - mx) : 0.f;
+      sum += sc[m];
+    }
+    sum = row16_sum(sum);
+#pragma unroll
+    for (int m = 0; m < PL; ++m) sc[m] = sc[m] / sum;
+  } else {
+#pragma unroll
+    for (int m = 0; m < PL; ++m) sc[m] = 1.f / (1.f + expf(-sc[m]));
+  }
+#pragma unroll
+  for (int m = 0; m < PL; ++m) {
+    const int e = gi + 16 * m;
+    sel[m] = (e < a.E) ? (a.bias ? sc[m] + a.bias[e] : sc[m]) : -INFINITY;
+  }
+  float picked = 0.f, my_v = 0.f;
+  int my_i = 0;
+  for (int k = 0; k < a.K; ++k) {
+    float bv = -INFINITY, bs = 0.f;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int m = 0; m < PL; ++m) {
+      const int e = gi + 16 * m;
+      if (e < a.E && (sel[m] > bv || (sel[m] == bv && e < bi))) {
+        bv = sel[m];
+        bi = e;
+        bs = sc[m];
+      }
+    }
+    argmax_step<kDppXor1>(bv, bi, bs);
+    argmax_step<kDppXor2>(bv, bi, bs);
+    argmax_step<kDppHalfMirror>(bv, bi, bs);
+    argmax_step<kDppMirror>(bv, bi, bs);
+    bi = min(max(bi, 0), a.E - 1);  // K <= E keeps a valid pick; stay in range regardless
+#pragma unroll
+    for (int m = 0; m < PL; ++m)
+      if (gi + 16 * m == bi) sel[m] = -INFINITY;
+    picked += bs;
+    if (gi == k) {
+      my_v = bs;
+      my_i = bi;
     }
   }
-  __syncthreads();
-
-  // ---- top-k: 16 lanes per token, lane i holds experts i + 16 m -------------
-  const int gi = l & 15;
-#pragma unroll 1
-  for (int pass = 0; pass < RT / (RWAVES * 4); ++pass) {
-    const int j = pass * (RWAVES * 4) + w * 4 + (l >> 4);  // token of this lane group
-    const int t = t0 + j;
-    float sc[PL], sel[PL];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int m = 0; m < PL; ++m) {
-      const int e = gi + 16 * m;
-      sc[m] = (e < a.E) ? lg[j * LGS + e] : -INFINITY;
-      mx = fmaxf(mx, sc[m]);
-    }
-    if (a.score_func == 0) {
-#pragma unroll
-      for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 16));
-      float sum = 0.f;
-#pragma unroll
-      for (int m = 0; m < PL; ++m) {
-        const int e = gi + 16 * m;
-        sc[m] = (e < a.E) ? expf(sc[m] - mx) : 0.f;
-        sum += sc[m];
-      }
-#pragma unroll
-      for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
-#pragma unroll
-      for (int m = 0; m < PL; ++m) sc[m] = sc[m] / sum;
-    } else {
-#pragma unroll
-      for (int m = 0; m < PL; ++m) sc[m] = 1.f / (1.f + expf(-sc[m]));
-    }
-#pragma unroll
-    for (int m = 0; m < PL; ++m) {
-      const int e = gi + 16 * m;
-      sel[m] = (e < a.E) ? (a.bias ? sc[m] + a.bias[e] : sc[m]) : -INFINITY;
-    }
-    float picked = 0.f, my_v = 0.f;
-    int my_i = 0;
-    for (int k = 0; k < a.K; ++k) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-#pragma unroll
-      for (int m = 0; m < PL; ++m) {
-        const int e = gi + 16 * m;
-        if (e < a.E && (sel[m] > bv || (sel[m] == bv && e < bi))) {
-          bv = sel[m];
-          bi = e;
-        }
-      }
-#pragma unroll
-      for (int off = 8; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(bv, off, 16);
-        const int oi = __shfl_xor(bi, off, 16);
-        if (ov > bv || (ov == bv && oi < bi)) {
-          bv = ov;
-          bi = oi;
-        }
-      }
-      bi = min(max(bi, 0), a.E - 1);  // K <= E keeps a valid pick; stay in range regardless
-      const int owner = bi & 15;
-      const int slot = bi >> 4;
-      float v = 0.f;
-#pragma unroll
-      for (int m = 0; m < PL; ++m)
-        if (m == slot) v = sc[m];
-      v = __shfl(v, owner, 16);
-#pragma unroll
-      for (int m = 0; m < PL; ++m)
-        if (m == slot && gi == owner) sel[m] = -INFINITY;
-      picked += v;
-      if (gi == k) {
-        my_v = v;
-        my_i = bi;
-      }
-    }
-    if (gi < a.K && t < a.T) {
-      float v = my_v;
-      if (a.renorm) v = v / (picked + a.eps);
-      a.scores[(int64_t)t * a.K + gi] = v * a.route_scale;
-      a.idx[(int64_t)t * a.K + gi] = my_i;
-    }
+  if (gi < a.K && valid) {
+    float v = my_v;
+    if (a.renorm) v = v / (picked + a.eps);
+    a.scores[(int64_t)t * a.K + gi] = v * a.route_scale;
+    a.idx[(int64_t)t * a.K + gi] = my_i;
   }
 }
 
 template <int EB>
-hipError_t launch_eb(const RouterArgs& a, hipStream_t stream) {
-  constexpr int EP = 32 * EB;
-  constexpr int lds = router_nst<EB>() * (RT + EP) * 128 + RT * (EP + 1) * 4;
+hipError_t launch_gemm_eb(const RouterGemmArgs& a, int S, hipStream_t stream) {
+  constexpr int lds = router_nst<EB>() * (RT + 32 * EB) * 128;
   static_assert(lds <= 160 * 1024, "router LDS");
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t err = hipFuncSetAttribute((const void*)router_fused_kernel<EB>,
+    hipError_t err = hipFuncSetAttribute((const void*)router_gemm_kernel<EB>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (err != hipSuccess) return err;
     attr_set = true;
   }
-  const int grid = (a.T + RT - 1) / RT;
-  hipLaunchKernelGGL(router_fused_kernel<EB>, dim3(grid), dim3(RTHREADS), lds, stream, a);
+  hipLaunchKernelGGL(router_gemm_kernel<EB>, dim3((a.T + RT - 1) / RT, S), dim3(RTHREADS), lds, stream, a);
   return hipGetLastError();
+}
+
+// Slices of D: enough gate-GEMM workgroups to give every CU one (each CU
+// then moves T*D*2/CUs bytes of x plus E*D*2/S of the weight), at most
+// kRouterMaxSplits (the partial logits cost 8*S*T*E bytes of traffic), each
+// slice at least 4 stages (256 columns) long.
+int router_splits(int T, int D) {
+  const int tiles = (T + RT - 1) / RT;
+  const int stages = D / RTK;
+  int S = (num_cus() + tiles - 1) / tiles;
+  S = max(1, min(min(S, kRouterMaxSplits), stages / 4));
+  const int per = (stages + S - 1) / S;
+  return (stages + per - 1) / per;  // no empty slice
 }
 
 }  // namespace
 
+size_t router_workspace_bytes(int64_t T, int E, int64_t D) {
+  if (T <= 0) return 0;
+  return (size_t)router_splits((int)T, (int)D) * (size_t)T * (size_t)E * sizeof(float) + 256;
+}
+
 hipError_t launch_router_fused(const void* x, const void* w, const float* bias, int T, int E, int D, int K,
                                int score_func, int renorm, float renorm_eps, float route_scale,
-                               float* top_scores, int64_t* top_idx, void* logits, hipStream_t stream) {
+                               float* top_scores, int64_t* top_idx, void* logits, void* ws,
+                               hipStream_t stream) {
   if (T == 0) return hipSuccess;
-  RouterArgs a;
-  a.x = (const bf16_t*)x;
-  a.w = (const bf16_t*)w;
-  a.bias = bias;
-  a.T = T;
-  a.E = E;
-  a.D = D;
-  a.K = K;
-  a.score_func = score_func;
-  a.renorm = renorm;
-  a.eps = renorm_eps;
-  a.route_scale = route_scale;
-  a.scores = top_scores;
-  a.idx = top_idx;
-  a.logits = (bf16_t*)logits;
-  if (E <= 32) return launch_eb<1>(a, stream);
-  if (E <= 64) return launch_eb<2>(a, stream);
-  if (E <= 128) return launch_eb<4>(a, stream);
-  return launch_eb<8>(a, stream);
+  const int S = router_splits(T, D);
+  RouterGemmArgs g;
+  g.x = (const bf16_t*)x;
+  g.w = (const bf16_t*)w;
+  g.T = T;
+  g.E = E;
+  g.D = D;
+  const int stages = D / RTK;
+  g.kstages = (stages + S - 1) / S;
+  g.part = (float*)ws;
+  hipError_t err;
+  if (E <= 32) err = launch_gemm_eb<1>(g, S, stream);
+  else if (E <= 64) err = launch_gemm_eb<2>(g, S, stream);
+  else if (E <= 128) err = launch_gemm_eb<4>(g, S, stream);
+  else err = launch_gemm_eb<8>(g, S, stream);
+  if (err != hipSuccess) return err;
+
+  RouterTopkArgs k;
+  k.part = g.part;
+  k.S = S;
+  k.T = T;
+  k.E = E;
+  k.K = K;
+  k.bias = bias;
+  k.score_func = score_func;
+  k.renorm = renorm;
+  k.eps = renorm_eps;
+  k.route_scale = route_scale;
+  k.scores = top_scores;
+  k.idx = top_idx;
+  k.logits = (bf16_t*)logits;
+  const dim3 grid((T + 15) / 16);
+  if (E <= 32) hipLaunchKernelGGL(router_topk_partials_kernel<2>, grid, dim3(256), 0, stream, k);
+  else if (E <= 64) hipLaunchKernelGGL(router_topk_partials_kernel<4>, grid, dim3(256), 0, stream, k);
+  else if (E <= 128) hipLaunchKernelGGL(router_topk_partials_kernel<8>, grid, dim3(256), 0, stream, k);
+  else hipLaunchKernelGGL(router_topk_partials_kernel<16>, grid, dim3(256), 0, stream, k);
+  return hipGetLastError();
 }
+
+static_assert(kRouterMaxE == 256, "EB = 8 covers 256 experts");
 
 }  // namespace ttamd

@@ -159,9 +159,11 @@ def router_fused(
     scores = torch.empty(T, top_k, dtype=torch.float32, device=dev)
     idx = torch.empty(T, top_k, dtype=torch.int64, device=dev)
     logits = torch.empty(T, E, dtype=_BF16, device=dev) if return_logits else None
+    ws = _ws(_lib.load().ttamd_router_workspace_bytes(T, E, D), dev)
     _lib.call(
         "ttamd_router_fused", _p(x), _p(w_router), _p(expert_bias), T, E, D, top_k, funcs[score_func],
-        int(bool(route_norm)), float(norm_eps), float(route_scale), _p(scores), _p(idx), _p(logits), _stream(dev),
+        int(bool(route_norm)), float(norm_eps), float(route_scale), _p(scores), _p(idx), _p(logits), _p(ws),
+        ws.numel(), _stream(dev),
     )
     if return_logits:
         return scores, idx, logits
