@@ -44,6 +44,7 @@ constexpr int kRouteWaves = kRouteThreads / kWave;
 constexpr int kRoutePerWave = 256;
 constexpr int kRouteChunk = kRouteWaves * kRoutePerWave;  // 1024
 constexpr int kScanThreads = 1024;
+constexpr int kScanBatch = 16;  // histogram entries per scan thread loaded at once
 
 template <typename IdxT>
 __device__ __forceinline__ int bucket_of(const IdxT* labels, int i, int E) {
@@ -84,8 +85,18 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
   const int per = (n + kScanThreads - 1) / kScanThreads;
   const int lo = min(tid * per, n);
   const int hi = min(lo + per, n);
+  // A thread's segment is loaded as one batch of independent loads (up to
+  // kScanBatch entries), not one dependent load per loop trip.
+  int seg[kScanBatch];
   int s = 0;
-  for (int i = lo; i < hi; ++i) s += hist[i];
+  if (per <= kScanBatch) {
+#pragma unroll
+    for (int j = 0; j < kScanBatch; ++j) seg[j] = (lo + j < hi) ? hist[lo + j] : 0;
+#pragma unroll
+    for (int j = 0; j < kScanBatch; ++j) s += seg[j];
+  } else {
+    for (int i = lo; i < hi; ++i) s += hist[i];
+  }
   const int incl = wave_inclusive_scan(s);
   const int w = tid / kWave, l = lane_id();
   if (l == kWave - 1) wave_sums[w] = incl;
@@ -97,11 +108,23 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
   }
   __syncthreads();
   int run = wave_sums[w] + incl - s;
-  for (int i = lo; i < hi; ++i) {
-    const int c = hist[i];
-    hist[i] = run;
-    if (i % nchunks == 0) sh_off[i / nchunks] = run;
-    run += c;
+  if (per <= kScanBatch) {
+#pragma unroll
+    for (int j = 0; j < kScanBatch; ++j) {
+      const int i = lo + j;
+      if (i < hi) {
+        hist[i] = run;
+        if (i % nchunks == 0) sh_off[i / nchunks] = run;
+        run += seg[j];
+      }
+    }
+  } else {
+    for (int i = lo; i < hi; ++i) {
+      const int c = hist[i];
+      hist[i] = run;
+      if (i % nchunks == 0) sh_off[i / nchunks] = run;
+      run += c;
+    }
   }
   if (tid == 0) sh_off[E + 1] = M;
   __syncthreads();
