@@ -79,7 +79,6 @@ constexpr int META_BYTES = TQ * 8;
 constexpr int IDX_OFF = LDS_BYTES + 3 * META_BYTES;
 constexpr int IDX_BYTES = TQ * 4;
 constexpr int LDS_TOTAL = IDX_OFF + 2 * IDX_BYTES;  // 154 KB
-static_assert(TQ / 64 <= WAVES, "one 64-row metadata chunk per wave");
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
@@ -130,14 +129,14 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   const int drow = l >> 3;
 
   // ---- DMA stream -----------------------------------------------------------
-  // Source-row ids of tile round r (gathered rows only): waves 0..TQ/64-1
-  // each move one 64-row chunk into slot r % 2.
+  // Source-row ids of tile round r (gathered rows only): 64-row chunk c of
+  // the tile is moved by wave c % WAVES into slot r % 2.
   auto load_ids = [&](int r) {
     const int tile = r * G + slot;
     const int4 ti = sload_int4(a.table + tile / a.np_tiles);
-    if (w < TQ / 64) {
-      const uint32_t q = (uint32_t)min(64 * w + l, ti.z - ti.y - 1);
-      dma4(q * 4, (uint64_t)(a.q_index + ti.y), lds0 + IDX_OFF + (uint32_t)((r & 1) * IDX_BYTES) + w * 256);
+    for (int c = w; c < TQ / 64; c += WAVES) {
+      const uint32_t q = (uint32_t)min(64 * c + l, ti.z - ti.y - 1);
+      dma4(q * 4, (uint64_t)(a.q_index + ti.y), lds0 + IDX_OFF + (uint32_t)((r & 1) * IDX_BYTES) + c * 256);
     }
   };
   int d_r = -1;  // tile round whose addresses are loaded
@@ -204,9 +203,9 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
       d_pbase = (uint64_t)(a.p + (int64_t)ti.x * a.p_estride + (int64_t)pt * TP * a.ldp);
     d_qbase = (uint64_t)(a.q + (GATHER ? 0 : (int64_t)ti.y * a.ldq));
     if constexpr (EPI == EPI_SCATTER) {
-      if (w < TQ / 64) {
-        const uint32_t q = (uint32_t)min(64 * w + l, qmax);
-        const uint32_t m = lds0 + LDS_BYTES + (uint32_t)((r % 3) * META_BYTES) + w * 256;
+      for (int c = w; c < TQ / 64; c += WAVES) {
+        const uint32_t q = (uint32_t)min(64 * c + l, qmax);
+        const uint32_t m = lds0 + LDS_BYTES + (uint32_t)((r % 3) * META_BYTES) + c * 256;
         if (a.dest) dma4(q * 4, (uint64_t)(a.dest + ti.y), m);
         if (a.row_scale) dma4(q * 4, (uint64_t)(a.row_scale + ti.y), m + TQ * 4);
       }
