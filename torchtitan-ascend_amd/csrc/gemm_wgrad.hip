@@ -47,6 +47,8 @@ constexpr int ROW_BYTES = 512;      // 256 bf16 columns of one row m
 constexpr int OP_BYTES = TK * ROW_BYTES;  // 32 KB per operand and stage
 constexpr int STAGE_BYTES = 2 * OP_BYTES;
 constexpr int LDS_BYTES = 2 * STAGE_BYTES;  // 128 KB
+constexpr int SLAB_BYTES = 32 * 128;        // per wave: one 32 x 64 bf16 output block
+constexpr int LDS_TOTAL = LDS_BYTES + WAVES * SLAB_BYTES;  // 160 KB
 constexpr int DMA_OP = OP_BYTES / 1024 / WAVES;  // 4 instructions per operand and wave
 constexpr int DMA_PER_STAGE = 2 * DMA_OP;
 
@@ -226,27 +228,49 @@ __global__ __launch_bounds__(THREADS, 1) void gg_wgrad_dma_kernel(const WgradDma
     int er32 = l & 31;
     asm volatile("" : "+v"(er32));
     const int half = l >> 5;
+    if (a.dw_fp32) {
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int n = t.nt * TQ + brow[j] + er32;
-      const bool n_ok = n < a.N;
-      const int64_t rowoff = ((int64_t)t.e * a.N + n) * a.K;
+      for (int j = 0; j < NJ; ++j) {
+        const int n = t.nt * TQ + brow[j] + er32;
+        const bool n_ok = n < a.N;
+        const int64_t rowoff = ((int64_t)t.e * a.N + n) * a.K;
 #pragma unroll
-      for (int pb = 0; pb < NPB; ++pb) {
-        if (t.kt * TP + arow[pb] < a.K) {
+        for (int pb = 0; pb < NPB; ++pb) {
+          if (t.kt * TP + arow[pb] < a.K) {
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int k = t.kt * TP + arow[pb] + 8 * g + 4 * half;
-            const floatx16_t& v = acc[pb][j];
-            if (n_ok) {
-              if (a.dw_fp32) {
+            for (int g = 0; g < 4; ++g) {
+              const int k = t.kt * TP + arow[pb] + 8 * g + 4 * half;
+              const floatx16_t& v = acc[pb][j];
+              if (n_ok)
                 *(float4*)((float*)a.dw + rowoff + k) = make_float4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
-              } else {
-                *(uint2*)((bf16_t*)a.dw + rowoff + k) =
-                    make_uint2(pack_bf16x2(v[4 * g], v[4 * g + 1]), pack_bf16x2(v[4 * g + 2], v[4 * g + 3]));
-              }
             }
           }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    } else if (t.kt * TP + arow[0] < a.K) {  // the wave's 64 columns are valid together
+      // bf16: each 32-row block goes through the wave's private 4 KB LDS
+      // slab (row r: 128 bytes, 16-byte chunk c at c ^ (r & 7)) and leaves
+      // as 4 stores of 8 whole 128-byte rows.
+      char* slab = smem + LDS_BYTES + w * SLAB_BYTES;
+      const int col = t.kt * TP + arow[0] + 8 * (l & 7);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+        for (int pb = 0; pb < NPB; ++pb)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const floatx16_t& v = acc[pb][j];
+            const int chunk = (4 * pb + g) ^ (er32 & 7);
+            *(uint2*)(slab + er32 * 128 + chunk * 16 + half * 8) =
+                make_uint2(pack_bf16x2(v[4 * g], v[4 * g + 1]), pack_bf16x2(v[4 * g + 2], v[4 * g + 3]));
+          }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 8 * i + (l >> 3);
+          const uint4 o = *(const uint4*)(slab + r * 128 + (((l & 7) ^ (r & 7)) << 4));
+          const int n = t.nt * TQ + brow[j] + r;
+          if (n < a.N) *(uint4*)((bf16_t*)a.dw + ((int64_t)t.e * a.N + n) * a.K + col) = o;
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -261,12 +285,12 @@ hipError_t launch_wgrad_dma(const WgradDmaArgs& a, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t err = hipFuncSetAttribute((const void*)gg_wgrad_dma_kernel,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, LDS_TOTAL);
     if (err != hipSuccess) return err;
     attr_set = true;
   }
   const int grid = (num_cus() + 7) & ~7;
-  hipLaunchKernelGGL(gg_wgrad_dma_kernel, dim3(grid), dim3(THREADS), LDS_BYTES, stream, a);
+  hipLaunchKernelGGL(gg_wgrad_dma_kernel, dim3(grid), dim3(THREADS), LDS_TOTAL, stream, a);
   return hipGetLastError();
 }
 
