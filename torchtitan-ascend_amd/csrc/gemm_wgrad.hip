@@ -265,10 +265,18 @@ __global__ __launch_bounds__(THREADS, 1) void gg_wgrad_dma_kernel(const WgradDma
             *(uint2*)(slab + er32 * 128 + chunk * 16 + half * 8) =
                 make_uint2(pack_bf16x2(v[4 * g], v[4 * g + 1]), pack_bf16x2(v[4 * g + 2], v[4 * g + 3]));
           }
+        lds_wait();  // the slab writes have landed
+        uint4 o4[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = 8 * i + (l >> 3);
-          const uint4 o = *(const uint4*)(slab + r * 128 + (((l & 7) ^ (r & 7)) << 4));
+          o4[i] = *(const uint4*)(slab + r * 128 + (((l & 7) ^ (r & 7)) << 4));
+        }
+        lds_wait();  // read before the next block overwrites the slab
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 8 * i + (l >> 3);
+          const uint4 o = o4[i];
           const int n = t.nt * TQ + brow[j] + r;
           if (n < a.N) *(uint4*)((bf16_t*)a.dw + ((int64_t)t.e * a.N + n) * a.K + col) = o;
         }
