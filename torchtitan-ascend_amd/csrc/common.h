@@ -64,6 +64,13 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
+// The wave's LDS writes (and reads) issued so far have completed.  A wave
+// that reads back LDS it has just written itself waits here first:
+// measured on gfx950, a ds_read following a masked run of ds_writes to the
+// same bytes could return the old contents.  Also a compiler barrier for
+// memory operations.
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 __device__ __forceinline__ uint64_t lanemask_lt() {
   const int l = lane_id();
   return (l == 0) ? 0ull : (~0ull >> (64 - l));

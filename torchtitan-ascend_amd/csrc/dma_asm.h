@@ -66,13 +66,6 @@ __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// The wave's LDS writes (and reads) issued so far have completed.  A wave
-// that reads back LDS it has just written itself must wait here first:
-// measured on gfx950, a ds_read following a masked run of ds_writes to the
-// same bytes could return the old contents.  Also a compiler barrier for
-// memory operations.
-__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
 // Wave-uniform loads through the scalar cache (read only).
 __device__ __forceinline__ int4 sload_int4(const int4* p) {
   i32x4_t v;

@@ -166,7 +166,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_rank_kernel(
     // touch the same counter, and other waves use their own row.
     if (valid && l == (int)__builtin_ctzll(mask))
       sh_cnt[w * E1 + b] += __builtin_popcountll(mask);
-    __builtin_amdgcn_wave_barrier();
+    lds_wait();  // the leader's counter update is visible to the next step
   }
   __syncthreads();
   // Running base of (wave w, bucket b) = chunk base + counts of earlier waves.
@@ -188,10 +188,10 @@ __global__ __launch_bounds__(kRouteThreads) void route_rank_kernel(
     const uint64_t mask = peers[s];
     int pos = 0;
     if (valid) pos = sh_cnt[w * E1 + b] + __builtin_popcountll(mask & lanemask_lt());
-    __builtin_amdgcn_wave_barrier();
+    lds_wait();  // every lane has read the counter before its leader updates it
     if (valid && l == (int)__builtin_ctzll(mask))
       sh_cnt[w * E1 + b] += __builtin_popcountll(mask);
-    __builtin_amdgcn_wave_barrier();
+    lds_wait();  // the leader's counter update is visible to the next step
     if (valid) {
       pos = min(max(pos, 0), M - 1);
       sorted_idx[pos] = g;
