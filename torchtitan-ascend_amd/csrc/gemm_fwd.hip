@@ -141,8 +141,19 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   };
   int d_r = -1;  // tile round whose addresses are loaded
   int d_qblk8 = 0;  // 8-row token blocks the MFMA reads: 4 * ceil(rows / 32)
+  int d_pmax = 0, d_qmax = 0;  // last valid weight / token row of the tile (tile-relative)
   uint64_t d_pbase = 0, d_qbase = 0;
-  uint32_t d_voff[DMA_PER_STAGE];
+  // Row-major operands: instruction i of wave w moves rows rr0 + 64 i with
+  // the same chunk permutation (row block 8 i + w has (8 i + w) & 7 = w), so
+  // its per-lane offset is recomputed at issue from two lane constants and
+  // the tile's uniform clamps, instead of occupying a register per
+  // instruction through the k loop.  Per-lane offsets that are not affine
+  // in i (transposed weights, gathered token rows) are kept per tile.
+  static_assert(WAVES == 8, "row block 8 i + w has chunk permutation term w");
+  const int rr0 = 8 * w + drow;
+  const uint32_t lch16 = (uint32_t)(((l & 7) ^ ((drow ^ w) & 7)) * 16);
+  uint32_t d_ptoff[PT ? DMA_P : 1];
+  uint32_t d_gqoff[GATHER ? DMA_Q : 1];
   auto dma_tile = [&](int r) {
     const int tile = r * G + slot;
     const int qt = tile / a.np_tiles;
@@ -151,27 +162,18 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     const int64_t ldp2 = a.ldp * 2;
     const int qmax = ti.z - ti.y - 1;
     d_qblk8 = 4 * ((ti.z - ti.y + 31) >> 5);
+    d_qmax = qmax;
+    if constexpr (PT) {
 #pragma unroll
-    for (int i = 0; i < DMA_P; ++i) {
-      if constexpr (PT) {
+      for (int i = 0; i < DMA_P; ++i) {
         // instruction i of wave w: rows 2 (WAVES i + w) and + 1, 32 chunks each
         const int row = 2 * (WAVES * i + w) + (l >> 5);
         const int lc = (l & 31) ^ ptswz(row);
         const int col = min(pt * TP + 8 * lc, a.n_p - 8) - pt * TP;
-        d_voff[i] = (uint32_t)(row * ldp2 + col * 2);
-        continue;
+        d_ptoff[i] = (uint32_t)(row * ldp2 + col * 2);
       }
-      const int rb = WAVES * i + w;
-      const int rr = 8 * rb + drow;  // tile weight row 0..255
-      const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
-      int prow;
-      if constexpr (EPI == EPI_SWIGLU) {
-        const int col = min(pt * 128 + (rr & 127), a.n_p - 1) - pt * 128;
-        prow = (rr < 128) ? col : (int)a.hidden + col;
-      } else {
-        prow = min(pt * TP + rr, a.n_p - 1) - pt * TP;
-      }
-      d_voff[i] = (uint32_t)(prow * ldp2 + lchunk * 16);
+    } else {
+      d_pmax = a.n_p - 1 - pt * (EPI == EPI_SWIGLU ? 128 : TP);
     }
     if constexpr (GATHER) {
       // Gathered rows: tile row rr reads source row q_index[row] / q_div,
@@ -179,21 +181,10 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
       const int* ids = (const int*)(smem + IDX_OFF + (r & 1) * IDX_BYTES);
 #pragma unroll
       for (int i = 0; i < DMA_Q; ++i) {
-        const int rb = WAVES * i + w;
-        const int rr = 8 * rb + drow;
-        const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
-        const int src = min(max(ids[min(rr, qmax)] / a.q_div, 0), a.n_q_in - 1);
-        d_voff[DMA_P + i] = (uint32_t)(src * a.ldq * 2 + lchunk * 16);
+        const int src = min(max(ids[min(rr0 + 64 * i, qmax)] / a.q_div, 0), a.n_q_in - 1);
+        d_gqoff[i] = (uint32_t)(src * a.ldq * 2) + lch16;
       }
       if (r + 1 < nmy) load_ids(r + 1);
-    } else {
-#pragma unroll
-      for (int i = 0; i < DMA_Q; ++i) {
-        const int rb = WAVES * i + w;
-        const int rr = 8 * rb + drow;  // tile token row 0..TQ-1
-        const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
-        d_voff[DMA_P + i] = (uint32_t)(min(rr, qmax) * a.ldq * 2 + lchunk * 16);
-      }
     }
     if constexpr (PT)
       d_pbase = (uint64_t)(a.p + (int64_t)ti.x * a.p_estride + (int64_t)pt * TP);
@@ -220,13 +211,31 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     const uint64_t pb = d_pbase + (PT ? (uint64_t)ks * TK * a.ldp * 2 : (uint64_t)ks * ROW_BYTES);
     const uint64_t qb = d_qbase + (uint64_t)ks * ROW_BYTES;
     const uint32_t st = lds0 + (uint32_t)((s & 1) * STAGE_BYTES) + w * 1024;
+    const uint32_t ldp2 = (uint32_t)a.ldp * 2u, ldq2 = (uint32_t)a.ldq * 2u;
 #pragma unroll
-    for (int i = 0; i < DMA_P; ++i) dma16(d_voff[i], pb, st + i * (WAVES * 1024));
+    for (int i = 0; i < DMA_P; ++i) {
+      uint32_t voff;
+      if constexpr (PT) {
+        voff = d_ptoff[i];
+      } else if constexpr (EPI == EPI_SWIGLU) {
+        // rows 0..127 gate, 128..255 up: tile row rr is weight row pt * 128 +
+        // (rr & 127), of the up half (hidden + ...) for rr >= 128
+        const int col = min(rr0 + 64 * (i & 1), d_pmax);
+        voff = (uint32_t)(i < 2 ? col : (int)a.hidden + col) * ldp2 + lch16;
+      } else {
+        voff = (uint32_t)min(rr0 + 64 * i, d_pmax) * ldp2 + lch16;
+      }
+      dma16(voff, pb, st + i * (WAVES * 1024));
+    }
     // Token rows past the tile's last 32-row block are never read: skip
     // their DMA (wave-uniform: instruction i moves row block WAVES * i + w).
 #pragma unroll
-    for (int i = 0; i < DMA_Q; ++i)
-      if (WAVES * i + w < d_qblk8) dma16(d_voff[DMA_P + i], qb, st + P_BYTES + i * (WAVES * 1024));
+    for (int i = 0; i < DMA_Q; ++i) {
+      if (WAVES * i + w < d_qblk8) {
+        const uint32_t voff = GATHER ? d_gqoff[GATHER ? i : 0] : (uint32_t)min(rr0 + 64 * i, d_qmax) * ldq2 + lch16;
+        dma16(voff, qb, st + P_BYTES + i * (WAVES * 1024));
+      }
+    }
   };
 
   // ---- fragment geometry -------------------------------------------------------
@@ -299,11 +308,11 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   issue(0);
   issue(1);
   wait_vm_barrier<0>();
-  Frag f0, f1;
 
   int s = 0;
   auto run_tile = [&](auto njv, int r, int row0, int row1, int pt) {
     constexpr int NJV = decltype(njv)::value;
+    Frag f0, f1;  // per tile: the first fragments are read at the tile's start
     read_frag(f0, s, 0, njv);
     constexpr int NJA = NJV > 0 ? NJV : 1;
     floatx16_t acc[NPB][NJA];
@@ -360,6 +369,8 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     //      loop, where every register is taken.
     int er32 = r32;
     asm volatile("" : "+v"(er32));
+    int ehalf = half;  // likewise for the lane's column half (store addresses)
+    asm volatile("" : "+v"(ehalf));
     // EPI_SWIGLU_BWD: saved pre-activation of token block jj
     auto load_h = [&](int jj, int pb, uint2 (&dst)[4][2]) {
       if constexpr (EPI == EPI_SWIGLU_BWD) {
@@ -496,12 +507,12 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
               uint32_t keep[2], recv[2];
 #pragma unroll
               for (int d = 0; d < 2; ++d) {
-                keep[d] = half ? pk[2 * c + 1][d] : pk[2 * c][d];
-                recv[d] = (uint32_t)__shfl_xor((int)(half ? pk[2 * c][d] : pk[2 * c + 1][d]), 32, 64);
+                keep[d] = ehalf ? pk[2 * c + 1][d] : pk[2 * c][d];
+                recv[d] = (uint32_t)__shfl_xor((int)(ehalf ? pk[2 * c][d] : pk[2 * c + 1][d]), 32, 64);
               }
-              const u32x4_t val = half ? u32x4_t{recv[0], recv[1], keep[0], keep[1]}
-                                       : u32x4_t{keep[0], keep[1], recv[0], recv[1]};
-              const int col = pt * TP + arow[pb] + 16 * c + 8 * half;
+              const u32x4_t val = ehalf ? u32x4_t{recv[0], recv[1], keep[0], keep[1]}
+                                        : u32x4_t{keep[0], keep[1], recv[0], recv[1]};
+              const int col = pt * TP + arow[pb] + 16 * c + 8 * ehalf;
               if (row_ok) {
                 if (a.accumulate) {
                   // add to the row already there (bf16 + bf16, one rounding)
