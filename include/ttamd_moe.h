@@ -438,6 +438,22 @@ int ttamd_grouped_mm_fp8_unpermute(const void* aq, const float* sa_t,
                                    void* workspace, size_t workspace_bytes,
                                    void* stream);
 
+/* ------------------------------------------------------------------------
+ * Kernel timing probe.  No counterpart in the reference: a measurement aid
+ * for benchmarks that need one kernel's duration from inside a larger op.
+ * ------------------------------------------------------------------------ */
+
+/*
+ * Arm the probe: the next forward grouped-GEMM launch of this process (any
+ * ttamd_grouped_mm* or ttamd_grouped_mm_fp8* entry point, bf16 or fp8)
+ * records start_event on its stream immediately before its main kernel
+ * (after the tile-table kernel) and end_event immediately after it, then
+ * disarms.  The events are caller-owned hipEvent_t created with timing
+ * enabled (torch.cuda.Event(enable_timing=True) after one record()).
+ * NULL for both disarms.  Not thread-safe: one arming thread per process.
+ */
+int ttamd_probe_next_gemm(void* start_event, void* end_event);
+
 #ifdef __cplusplus
 }
 #endif

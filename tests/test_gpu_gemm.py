@@ -225,3 +225,33 @@ def test_grouped_mm_full_size_linearity_and_samples(ops):
     xs = to_np(x[torch.from_numpy(rows).to(DEV)])
     ref = np.stack([xs[i] @ to_np(w[int(e)]).T for i, e in enumerate(e_of)])
     assert O.max_rel_err(to_np(out[torch.from_numpy(rows).to(DEV)]), ref) < TOL
+
+
+def test_probe_times_one_gemm_kernel(ops):
+    """The timing probe brackets exactly the next forward GEMM launch: its
+    span lies inside the op's own event span, and the probe disarms after
+    one launch (a second op leaves the events untouched)."""
+    rng = np.random.default_rng(5)
+    M, E, N, K = 4096, 8, 512, 1024
+    counts = _counts("random", M, E, rng)
+    x, w, offs = bf16_dev(rand_bf16(rng, (M, K))), bf16_dev(rand_bf16(rng, (E, N, K), 0.05)), _offs(counts)
+    announce("probe_next_gemm")
+    ops.grouped_mm(x, w, offs)  # warm
+    p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    o0, o1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ops.probe_next_gemm(p0, p1)
+    o0.record()
+    out = ops.grouped_mm(x, w, offs)
+    o1.record()
+    torch.cuda.synchronize()
+    probe_ms, op_ms = p0.elapsed_time(p1), o0.elapsed_time(o1)
+    assert 0.0 < probe_ms <= op_ms
+    assert O.max_rel_err(to_np(out), _gmm_ref(to_np(x), to_np(w), counts)) < TOL
+    # disarmed: the next op does not record the probe events again
+    marker = torch.cuda.Event(enable_timing=True)
+    marker.record()
+    ops.grouped_mm(x, w, offs)
+    torch.cuda.synchronize()
+    assert p1.elapsed_time(marker) > 0.0
+    with pytest.raises(ValueError):
+        ops.probe_next_gemm(p0, None)

@@ -350,6 +350,13 @@ int ttamd_moe_group_labels(const int32_t* counts_group, int num_groups, int num_
                    fn);
 }
 
+int ttamd_probe_next_gemm(void* start_event, void* end_event) {
+  REQUIRE((start_event == nullptr) == (end_event == nullptr),
+          "ttamd_probe_next_gemm: give both events or neither");
+  ttamd::gemm_probe_arm((hipEvent_t)start_event, (hipEvent_t)end_event);
+  return 0;
+}
+
 size_t ttamd_gemm_workspace_bytes(int64_t num_rows, int num_experts) {
   if (num_rows < 0 || num_experts < 1) return 0;
   return ttamd::gemm_workspace_bytes(num_rows, num_experts);

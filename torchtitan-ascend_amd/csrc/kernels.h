@@ -40,6 +40,9 @@ hipError_t launch_router_fused(const void* x, const void* w, const float* bias, 
 // gemm.hip
 int gemm_max_qtiles(int M, int E);
 size_t gemm_workspace_bytes(int64_t M, int E);
+// The next forward grouped-GEMM launch records these events around its main
+// kernel on its stream, then the probe disarms (nullptr, nullptr: disarm).
+void gemm_probe_arm(hipEvent_t start, hipEvent_t end);
 hipError_t launch_grouped_mm(const void* x, const void* w, const int* offs, int M, int E, int N,
                              int K, void* out, void* ws, hipStream_t stream);
 hipError_t launch_grouped_mm_swiglu(const void* x, const void* w13, const int* offs, int M,

@@ -412,6 +412,23 @@ def _gemm_ws(M: int, E: int, dev: torch.device) -> torch.Tensor:
     return _ws(_lib.load().ttamd_gemm_workspace_bytes(M, E), dev)
 
 
+def probe_next_gemm(start: "torch.cuda.Event | None", end: "torch.cuda.Event | None") -> None:
+    """Arm the kernel timing probe (ttamd_probe_next_gemm): the next forward
+    grouped-GEMM op (grouped_mm*, bf16 or fp8) records `start` and `end` on its
+    stream immediately around its main kernel, excluding the tile-table
+    kernel before it.  The events need enable_timing=True; they are recorded
+    once here so that the HIP events exist.  None, None disarms."""
+    if (start is None) != (end is None):
+        raise ValueError("probe_next_gemm: give both events or neither")
+    if start is None:
+        _lib.call("ttamd_probe_next_gemm", None, None)
+        return
+    for e in (start, end):
+        if not e.cuda_event:
+            e.record()
+    _lib.call("ttamd_probe_next_gemm", ctypes.c_void_p(start.cuda_event), ctypes.c_void_p(end.cuda_event))
+
+
 def _offs(offs: torch.Tensor, dev: torch.device) -> torch.Tensor:
     _same_device(dev, offs=offs)
     if offs.dtype != torch.int32:
