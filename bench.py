@@ -182,8 +182,18 @@ def main():
             with torch.no_grad():
                 return step_forward(ev)
 
-    for _ in range(args.warmup):
-        step()
+    # Per-step stage events are created (first record) during the warmup, so
+    # the timed steps only record them.
+    step_events = [{} for _ in range(args.steps)]
+    for i in range(args.warmup):
+        step(step_events[i % args.steps])
+    names = list(step_events[0]) if step_events[0] else []
+    for ev in step_events:  # dicts the warmup did not reach (warmup < steps)
+        for name in names:
+            if name not in ev:
+                ev[name] = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                ev[name][0].record()
+                ev[name][1].record()
     torch.cuda.synchronize()
     log("warmup done")
     # Timed region: K steps between two synchronisations.  Each step records
@@ -199,14 +209,11 @@ def main():
         for e in pair:
             e.record()  # creates the HIP events outside the timed region
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    step_events = []
     torch.cuda.synchronize()
     start.record()
     for i in range(args.steps):
-        ev = {}
         ops.probe_next_gemm(*probes[i])
-        step(ev)
-        step_events.append(ev)
+        step(step_events[i])
     end.record()
     torch.cuda.synchronize()
     ops.probe_next_gemm(None, None)
