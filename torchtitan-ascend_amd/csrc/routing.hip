@@ -390,6 +390,11 @@ hipError_t launch_invert_perm(const int* sorted, int M, int* inv, hipStream_t st
 }
 
 // out[t] = sum_k w(t,k) * in[j(t,k)],  j = inverse ? inverse[t*topk+k] : t*topk+k.
+// The K rows of a chunk are loaded kCombineBatch at a time, all loads of a
+// batch issued before any of them is used, so a thread keeps up to
+// kCombineBatch 16-byte loads in flight; the sum runs in k order.
+constexpr int kCombineBatch = 8;
+
 __global__ __launch_bounds__(kMoveThreads) void combine_kernel(
     const uint4* __restrict__ in, const int* __restrict__ inverse,
     const float* __restrict__ probs, int T, int topk, int M, int cpr,
@@ -400,15 +405,29 @@ __global__ __launch_bounds__(kMoveThreads) void combine_kernel(
     const int t = idx / cpr;
     const int c = idx - t * cpr;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int k = 0; k < topk; ++k) {
-      const int s = t * topk + k;
-      int j = inverse ? inverse[s] : s;
-      j = min(max(j, 0), M - 1);
-      const float w = probs ? probs[s] : 1.f;
-      float f[8];
-      unpack8(in[(size_t)j * cpr + c], f);
+    for (int k0 = 0; k0 < topk; k0 += kCombineBatch) {
+      uint4 v[kCombineBatch];
+      float w[kCombineBatch];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += w * f[i];
+      for (int b = 0; b < kCombineBatch; ++b) {
+        const int k = k0 + b;
+        if (k < topk) {
+          const int s = t * topk + k;
+          int j = inverse ? inverse[s] : s;
+          j = min(max(j, 0), M - 1);
+          w[b] = probs ? probs[s] : 1.f;
+          v[b] = in[(size_t)j * cpr + c];
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < kCombineBatch; ++b) {
+        if (k0 + b < topk) {
+          float f[8];
+          unpack8(v[b], f);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] += w[b] * f[i];
+        }
+      }
     }
     out[idx] = pack8(acc);
   }
