@@ -206,30 +206,49 @@ __device__ __forceinline__ void argmax_step(float& bv, int& bi, float& bs) {
   }
 }
 
-// 16 lanes per token (lane i holds experts i + 16 m), 4 tokens per wave,
-// 16 tokens per workgroup.
+// 16 lanes per token, 4 tokens per wave, 16 tokens per workgroup.  Lane i
+// holds experts in runs of G = min(PL, 4) consecutive ids,
+// e(m) = G i + m % G + 16 G (m / G), so each run of partials is one 4G-byte
+// load (the 16 lanes of a token read 64 G contiguous bytes per run).
 template <int PL>
 __global__ __launch_bounds__(256) void router_topk_partials_kernel(const RouterTopkArgs a) {
+  constexpr int G = PL < 4 ? PL : 4;
   const int l = threadIdx.x & 63;
   const int gi = l & 15;
   const int t = blockIdx.x * 16 + (threadIdx.x >> 4);
   const bool valid = t < a.T;
   const int tt = valid ? t : a.T - 1;
+  auto eid = [&](int m) { return G * gi + m % G + 16 * G * (m / G); };
   float sc[PL], sel[PL];
   // every partial first (one batch of independent loads), then the sums in
   // split order
   float pv[kRouterMaxSplits][PL];
+  const bool vec = (a.E % G) == 0;  // runs never straddle E and stay aligned
 #pragma unroll
   for (int s = 0; s < kRouterMaxSplits; ++s)
 #pragma unroll
-    for (int m = 0; m < PL; ++m) {
-      const int e = gi + 16 * m;
-      pv[s][m] = (s < a.S && e < a.E) ? a.part[((int64_t)s * a.T + tt) * a.E + e] : 0.f;
+    for (int m0 = 0; m0 < PL; m0 += G) {
+      const int e0 = eid(m0);
+      const float* src = a.part + ((int64_t)s * a.T + tt) * a.E + e0;
+      if (s < a.S && vec && e0 < a.E) {
+        if constexpr (G == 4) {
+          const float4 v = *(const float4*)src;
+          pv[s][m0] = v.x; pv[s][m0 + 1] = v.y; pv[s][m0 + 2] = v.z; pv[s][m0 + 3] = v.w;
+        } else if constexpr (G == 2) {
+          const float2 v = *(const float2*)src;
+          pv[s][m0] = v.x; pv[s][m0 + 1] = v.y;
+        } else {
+          pv[s][m0] = src[0];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < G; ++i) pv[s][m0 + i] = (s < a.S && e0 + i < a.E) ? src[i] : 0.f;
+      }
     }
   float mx = -INFINITY;
 #pragma unroll
   for (int m = 0; m < PL; ++m) {
-    const int e = gi + 16 * m;
+    const int e = eid(m);
     float z = -INFINITY;
     if (e < a.E) {
       z = pv[0][m];
@@ -247,7 +266,7 @@ __global__ __launch_bounds__(256) void router_topk_partials_kernel(const RouterT
     float sum = 0.f;
 #pragma unroll
     for (int m = 0; m < PL; ++m) {
-      const int e = gi + 16 * m;
+      const int e = eid(m);
       sc[m] = (e < a.E) ? expf(sc[m] - mx) : 0.f;
       sum += sc[m];
     }
@@ -260,7 +279,7 @@ __global__ __launch_bounds__(256) void router_topk_partials_kernel(const RouterT
   }
 #pragma unroll
   for (int m = 0; m < PL; ++m) {
-    const int e = gi + 16 * m;
+    const int e = eid(m);
     sel[m] = (e < a.E) ? (a.bias ? sc[m] + a.bias[e] : sc[m]) : -INFINITY;
   }
   float picked = 0.f, my_v = 0.f;
@@ -270,7 +289,7 @@ __global__ __launch_bounds__(256) void router_topk_partials_kernel(const RouterT
     int bi = 0x7fffffff;
 #pragma unroll
     for (int m = 0; m < PL; ++m) {
-      const int e = gi + 16 * m;
+      const int e = eid(m);
       if (e < a.E && (sel[m] > bv || (sel[m] == bv && e < bi))) {
         bv = sel[m];
         bi = e;
@@ -284,7 +303,7 @@ __global__ __launch_bounds__(256) void router_topk_partials_kernel(const RouterT
     bi = min(max(bi, 0), a.E - 1);  // K <= E keeps a valid pick; stay in range regardless
 #pragma unroll
     for (int m = 0; m < PL; ++m)
-      if (gi + 16 * m == bi) sel[m] = -INFINITY;
+      if (eid(m) == bi) sel[m] = -INFINITY;
     picked += bs;
     if (gi == k) {
       my_v = bs;
