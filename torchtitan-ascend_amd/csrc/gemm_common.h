@@ -13,7 +13,11 @@ enum Epi {
   EPI_SWIGLU_BWD = 3,  // dh from dA = acc and the saved pre-activation h
 };
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
+// 1 / (1 + exp(-x)) with the hardware reciprocal (1 ulp) in place of an
+// IEEE division (about ten instructions): the GEMM epilogues that use it are
+// VALU-bound and round their results to bf16.
+__device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+__device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 
 // Token-row tiles: table[i] = {expert, first row, end row, 0}, at most
 // kFwdTileRows rows (bf16 forward and dgrad) or kFp8TileRows (fp8).  The

@@ -457,7 +457,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
                   if (uc > L) { uc = L; mu = 0.f; }
                   if (uc < -L) { uc = -L; mu = 0.f; }
                 }
-                const float sig = 1.f / (1.f + __expf(-gc));
+                const float sig = sigmoid_f(gc);
                 const float sv = gc * sig;
                 const float ds = sig * (1.f + gc * (1.f - sig));
                 dg[i] = gd * uc * ds * mg;
@@ -484,7 +484,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
           if (a.dest) orow_idx = min(max(meta[qrow], 0), a.n_dest - 1);
           if (a.row_scale) {
             sc = __int_as_float(meta[TQ + qrow]);
-            if (a.scale_sigmoid) sc = 1.f / (1.f + __expf(-sc));
+            if (a.scale_sigmoid) sc = sigmoid_f(sc);
           }
         }
         bf16_t* orow = a.out + (int64_t)orow_idx * a.ldo;
