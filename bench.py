@@ -296,6 +296,19 @@ def main():
         },
     }
 
+    if not fp8:
+        # The bf16 MFMA rate this GPU sustains on random operands (the GEMM's
+        # k loop alone, no memory traffic): the practical ceiling for
+        # `roofline.achieved`, measured after the timed region.
+        ceiling = ops.mfma_loop_ceiling(dev)
+        result["mfma_loop_ceiling"] = {
+            "tflops": round(ceiling, 1),
+            "frac_of_peak": round(ceiling / peak, 4),
+            "roofline_achieved_frac_of_ceiling": round(result["roofline"]["achieved"] / ceiling, 4),
+            "probe": "ttamd_probe_mfma_loop: gg_fwd k loop (LDS fragment reads + v_mfma_f32_32x32x16_bf16 + "
+                     "stage barriers) on pseudo-random bf16 data, no global memory traffic",
+        }
+        log(f"mfma loop ceiling on random data: {ceiling:.1f} TFLOP/s")
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, cfg, x, w13, w2, router)
     print(json.dumps(result), flush=True)

@@ -454,6 +454,17 @@ int ttamd_grouped_mm_fp8_unpermute(const void* aq, const float* sa_t,
  */
 int ttamd_probe_next_gemm(void* start_event, void* end_event);
 
+/*
+ * MFMA ceiling probe: launches, on `stream`, the forward grouped GEMM's k
+ * loop with everything but the LDS fragment reads, the MFMAs and the stage
+ * barriers taken out, on pseudo-random bf16 data held in LDS (one
+ * workgroup per CU, `stages` 64-wide k stages each).  *flops receives the
+ * launch's flop count; time it with events to get the bf16 MFMA rate the GPU
+ * sustains on random operands (its power management lowers the clock for
+ * them).  sink: 4 bytes of device memory (never written in practice).
+ */
+int ttamd_probe_mfma_loop(int64_t stages, double* flops, void* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

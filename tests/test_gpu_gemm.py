@@ -255,3 +255,21 @@ def test_probe_times_one_gemm_kernel(ops):
     assert p1.elapsed_time(marker) > 0.0
     with pytest.raises(ValueError):
         ops.probe_next_gemm(p0, None)
+
+
+def test_mfma_loop_probe(ops):
+    """The MFMA ceiling probe runs and reports a rate below the dense bf16
+    peak; its flop count follows the launch geometry."""
+    import ctypes
+    from importlib import import_module
+    lib = import_module(ops.__name__.rsplit(".", 1)[0] + "._lib").load()
+    announce("probe_mfma_loop")
+    sink = torch.zeros(1, device=DEV)
+    flops = ctypes.c_double(0.0)
+    assert lib.ttamd_probe_mfma_loop(64, ctypes.byref(flops), ctypes.c_void_p(sink.data_ptr()),
+                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)) == 0
+    torch.cuda.synchronize()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert flops.value == cus * 8 * 64 * 4 * 2 * 5 * 32768
+    rate = ops.mfma_loop_ceiling(stages=256, reps=3, warmup=2)
+    assert 50.0 < rate < 2600.0

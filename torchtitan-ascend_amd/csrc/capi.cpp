@@ -357,6 +357,14 @@ int ttamd_probe_next_gemm(void* start_event, void* end_event) {
   return 0;
 }
 
+int ttamd_probe_mfma_loop(int64_t stages, double* flops, void* sink, void* stream) {
+  const char* fn = "ttamd_probe_mfma_loop";
+  REQUIRE(stages >= 1 && stages <= (1LL << 24), "%s: stages must be in [1, 2^24]", fn);
+  REQUIRE(sink != nullptr, "%s: sink is null", fn);
+  if (flops) *flops = ttamd::probe_mfma_loop_flops(stages);
+  return check_hip(ttamd::launch_probe_mfma_loop(stages, (float*)sink, (hipStream_t)stream), fn);
+}
+
 size_t ttamd_gemm_workspace_bytes(int64_t num_rows, int num_experts) {
   if (num_rows < 0 || num_experts < 1) return 0;
   return ttamd::gemm_workspace_bytes(num_rows, num_experts);

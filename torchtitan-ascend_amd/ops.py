@@ -429,6 +429,26 @@ def probe_next_gemm(start: "torch.cuda.Event | None", end: "torch.cuda.Event | N
     _lib.call("ttamd_probe_next_gemm", ctypes.c_void_p(start.cuda_event), ctypes.c_void_p(end.cuda_event))
 
 
+def mfma_loop_ceiling(device: torch.device | None = None, stages: int = 4096, reps: int = 10,
+                      warmup: int = 20) -> float:
+    """bf16 MFMA rate (TFLOP/s) of the grouped GEMM's k loop alone on random
+    operands (ttamd_probe_mfma_loop), timed with events on the current
+    stream: the ceiling a bf16 GEMM on realistic data approaches on this GPU."""
+    dev = torch.device(device or "cuda")
+    sink = torch.zeros(1, dtype=torch.float32, device=dev)
+    flops = ctypes.c_double(0.0)
+    st = _stream(dev)
+    for _ in range(warmup):
+        _lib.call("ttamd_probe_mfma_loop", stages, ctypes.byref(flops), _p(sink), st)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        _lib.call("ttamd_probe_mfma_loop", stages, ctypes.byref(flops), _p(sink), st)
+    e1.record()
+    torch.cuda.synchronize(dev)
+    return flops.value * reps / (e0.elapsed_time(e1) * 1e-3) / 1e12
+
+
 def _offs(offs: torch.Tensor, dev: torch.device) -> torch.Tensor:
     _same_device(dev, offs=offs)
     if offs.dtype != torch.int32:
