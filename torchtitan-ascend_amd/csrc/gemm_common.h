@@ -66,7 +66,7 @@ struct FwdGemm {
   int scale_sigmoid;  // EPI_SCATTER: the row scale is sigmoid(row_scale[j])
 };
 
-// Kernel arguments of the forward GEMMs (gemm_fwd.hip, gemm_ring.hip).
+// Kernel arguments of the forward and dgrad GEMMs (gemm_fwd.hip).
 struct FwdArgs {
   const bf16_t* q;  // activations [M][kred], or [n_q_in][kred] gathered through q_index
   int64_t ldq;
