@@ -227,6 +227,61 @@ def test_grouped_mm_full_size_linearity_and_samples(ops):
     assert O.max_rel_err(to_np(out[torch.from_numpy(rows).to(DEV)]), ref) < TOL
 
 
+@pytest.mark.parametrize("M,E,kind", [(20000, 32, "zipf"), (65536, 128, "random"), (3000, 8, "one"), (65536, 128, "uniform")])
+def test_tile_table_covers_every_row_once(ops, M, E, kind):
+    """The token-tile table the GEMM walks (workspace: int count, then one
+    int4 {expert, first row, end row, 0} per tile from byte 16): every row
+    in exactly one tile of its expert, an expert's c rows in ceil(c/320)
+    tiles of one height (a multiple of 32, the last tile shorter), tiles in
+    expert then row order; entries past the count marked -1."""
+    rng = np.random.default_rng(M + E)
+    counts = _counts(kind, M, E, rng)
+    if kind == "random":  # near-uniform around M/E, as top-8 routing gives
+        counts = rng.multinomial(M, np.full(E, 1.0 / E))
+    offs = _offs(counts)
+    N, K = 128, 64
+    x, w = bf16_dev(rand_bf16(rng, (M, K))), bf16_dev(rand_bf16(rng, (E, N, K), 0.05))
+    lib = ops._lib.load()
+    wsb = int(lib.ttamd_gemm_workspace_bytes(M, E))
+    ws = torch.full((wsb,), 0x7F, dtype=torch.uint8, device=DEV)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    announce(f"tile table M={M} E={E} {kind}")
+    ops._lib.call("ttamd_grouped_mm", ops._p(x), ops._p(w), ops._p(offs), M, E, N, K, ops._p(out), ops._p(ws), wsb,
+                  ops._stream(DEV))
+    torch.cuda.synchronize()
+    raw = ws.cpu().numpy()
+    count = int(raw[:4].view(np.int32)[0])
+    max_tiles = M // 128 + E + 1
+    tab = raw[16 : 16 + 16 * max_tiles].view(np.int32).reshape(max_tiles, 4)
+    ends = np.cumsum(counts)
+    starts = ends - counts
+    height = np.zeros(E, np.int64)
+    ntiles = np.zeros(E, np.int64)
+    for e in range(E):
+        c = int(counts[e])
+        if c:
+            n0 = -(-c // 320)
+            height[e] = (-(-c // n0) + 31) // 32 * 32
+            ntiles[e] = -(-c // height[e])
+    assert count == ntiles.sum()
+    assert (tab[count:, 0] == -1).all()
+    t = tab[:count]
+    assert ((t[:, 0] >= 0) & (t[:, 0] < E)).all()
+    ex = t[:, 0]
+    assert (t[:, 1] >= starts[ex]).all() and (t[:, 2] <= ends[ex]).all() and (t[:, 1] < t[:, 2]).all()
+    assert (t[:, 2] - t[:, 1] <= height[ex]).all()
+    cover = np.zeros(M, np.int64)
+    for r0, r1 in t[:, 1:3]:
+        cover[r0:r1] += 1
+    assert (cover == 1).all()
+    assert (np.diff(t[:, 1]) > 0).all() and (np.diff(ex) >= 0).all(), "tiles out of expert / row order"
+    for e in np.unique(ex):
+        idx = np.nonzero(ex == e)[0]
+        assert (t[idx[:-1], 2] - t[idx[:-1], 1] == height[e]).all()
+    ref = _gmm_ref(to_np(x), to_np(w), counts)
+    assert O.max_rel_err(to_np(out), ref) < TOL
+
+
 def test_probe_times_one_gemm_kernel(ops):
     """The timing probe brackets exactly the next forward GEMM launch: its
     span lies inside the op's own event span, and the probe disarms after

@@ -502,16 +502,21 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
             // columns 8g + 4h .. + 3 of group g.  Swapping one group each
             // way leaves lane half h with columns 16c + 8h .. + 7 (c = 0, 1),
             // so every store is 16 bytes and 32 contiguous bytes per row.
+            // v_permlane32_swap(x, y) exchanges x of lanes 32..63 with y of
+            // lanes 0..31: with x = group 2c and y = group 2c + 1, the low
+            // half ends with {own 2c, partner's 2c} (columns 16c .. + 7) and
+            // the high half with {partner's 2c + 1, own 2c + 1}
+            // (columns 16c + 8 .. + 15), both in (x, y) order.
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
-              uint32_t keep[2], recv[2];
+              uint32_t x[2], y[2];
 #pragma unroll
               for (int d = 0; d < 2; ++d) {
-                keep[d] = ehalf ? pk[2 * c + 1][d] : pk[2 * c][d];
-                recv[d] = (uint32_t)__shfl_xor((int)(ehalf ? pk[2 * c][d] : pk[2 * c + 1][d]), 32, 64);
+                const auto sw = __builtin_amdgcn_permlane32_swap(pk[2 * c][d], pk[2 * c + 1][d], false, false);
+                x[d] = sw[0];
+                y[d] = sw[1];
               }
-              const u32x4_t val = ehalf ? u32x4_t{recv[0], recv[1], keep[0], keep[1]}
-                                        : u32x4_t{keep[0], keep[1], recv[0], recv[1]};
+              const u32x4_t val = u32x4_t{x[0], x[1], y[0], y[1]};
               const int col = pt * TP + arow[pb] + 16 * c + 8 * ehalf;
               if (row_ok) {
                 if (a.accumulate) {
