@@ -13,18 +13,23 @@
 //
 // Tile: up to 256 token rows (Q) x 128 weight rows (P); k in stages of 128
 // (one scale block, one 128-byte line per row).
-//   * 4 waves, one per SIMD, 2 x 2: wave (wq, wp) owns token rows 128wq.. and
+//   * 8 waves, two per SIMD, 4 x 2: wave (wq, wp) owns token rows 64wq.. and
 //     64 weight rows (SWIGLU: 32 gate rows and the 32 matching up rows), i.e.
-//     4 x 8 blocks of v_mfma_scale_f32_16x16x128_f8f6f4 (unit hardware
+//     4 x 4 blocks of v_mfma_scale_f32_16x16x128_f8f6f4 (unit hardware
 //     scales): one MFMA covers a block's whole k = 128 scale block, and its
 //     partial sum goes straight into the fp32 accumulator times sx * sw, so
 //     the fp32 block scales are applied once per block as in the dequantised
-//     form, with no partial sums kept across MFMAs.
+//     form, with no partial sums kept across MFMAs.  The scale FMAs are VALU
+//     work of about half the MFMA time; with two waves per SIMD one wave's
+//     FMAs run under the other's MFMAs, and 64 accumulator registers per wave
+//     leave the partial sums in VGPRs (with one wave per SIMD and 128
+//     accumulators each FMA also needed an AGPR read).
 //   * Three LDS stages of 50 KB: 16 KB weight rows + 32 KB token rows (DMA,
 //     global_load_lds_dwordx4, 8 rows per instruction, XOR-swizzled 16-byte
-//     chunks as in the bf16 kernel), 1 KB of token-row scales and one copy of
-//     the stage's weight-block scales per wave.  The barrier at the top of
-//     stage s waits for stage s + 1, so while stage s is computed from
+//     chunks as in the bf16 kernel), 1 KB of token-row scales (waves 0-3) and
+//     the stage's weight-block scales (waves 4-7 each load a copy, so every
+//     wave issues the same DMA count; all read wave 4's).  The barrier at the
+//     top of stage s waits for stage s + 1, so while stage s is computed from
 //     registers, each fragment register is refilled with stage s + 1 right
 //     after its last use.
 //   * Persistent workgroups, XCD-aware slots, flattened (tile, stage) DMA
@@ -43,18 +48,18 @@ constexpr int TQ = 256;  // token rows
 constexpr int TP = 128;  // weight rows
 constexpr int TKB = 128;  // k per stage (bytes per row)
 constexpr int NSTAGE = 3;
-constexpr int FTHREADS = 256;
-constexpr int NJ = 4;   // 32-row token blocks per wave
-constexpr int NPB = 2;  // 32-row weight blocks per wave
+constexpr int WAVES = 8;
+constexpr int FTHREADS = 64 * WAVES;
 constexpr int P_BYTES = TP * TKB;  // 16 KB
 constexpr int Q_BYTES = TQ * TKB;  // 32 KB
 constexpr int SX_OFF = P_BYTES + Q_BYTES;
 constexpr int SW_OFF = SX_OFF + TQ * 4;
 constexpr int STAGE_BYTES = SW_OFF + 4 * 256;     // 50 KB
 constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;   // 150 KB
-constexpr int DMA_P = TP / 8 / 4;                 // 4
-constexpr int DMA_Q = TQ / 8 / 4;                 // 8
-constexpr int DMA_PER_STAGE = DMA_P + DMA_Q + 2;  // + scales of rows and weight blocks
+constexpr int DMA_P = TP / 8 / WAVES;             // 2
+constexpr int DMA_Q = TQ / 8 / WAVES;             // 4
+constexpr int DMA_PER_STAGE = DMA_P + DMA_Q + 1;  // + row scales (waves 0-3) or weight-block scales (4-7)
+static_assert(TQ == 4 * 64 && TP == 2 * 64 && WAVES == 8, "wave layout: 4 token x 2 weight quarters");
 // EPI_SCATTER metadata slots (tile round % 4): tile r's slot is written
 // when its first stage is issued, three stages ahead, so with one-stage
 // tiles (k = 128) the writer runs three rounds ahead of the epilogue that
@@ -72,7 +77,7 @@ __device__ __forceinline__ int cswz(int r) { return (r ^ (r >> 3)) & 7; }
 // Fragments of one stage (k = 128): NPB16 weight blocks and NJ16 token
 // blocks of 16 rows; lane l holds bytes 32 (l / 16) .. + 31 of row l % 16.
 constexpr int NPB16 = 4;
-constexpr int NJ16 = 8;
+constexpr int NJ16 = 4;
 struct Frag16 {
   i32x8_t a[NPB16];
   i32x8_t b[NJ16];
@@ -99,9 +104,10 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
 
   // ---- DMA stream -----------------------------------------------------------
   int d_r = -1;
-  uint64_t d_pbase = 0, d_qbase = 0, d_sxbase = 0, d_swbase = 0;
+  uint64_t d_pbase = 0, d_qbase = 0, d_scbase = 0, d_scstep = 0;
   uint32_t d_voff[DMA_P + DMA_Q];
-  uint32_t d_sxoff = 0, d_swoff = 0;
+  uint32_t d_scoff = 0;
+  const uint32_t d_sclds = (w < 4) ? (uint32_t)(SX_OFF + w * 256) : (uint32_t)(SW_OFF + (w - 4) * 256);
   auto dma_tile = [&](int r) {
     const int tile = r * G + slot;
     const int qt = tile / a.np_tiles;
@@ -110,7 +116,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
     const int qmax = ti.z - ti.y - 1;
 #pragma unroll
     for (int i = 0; i < DMA_P; ++i) {
-      const int rb = 4 * i + w;
+      const int rb = WAVES * i + w;
       const int rr = 8 * rb + drow;  // tile weight row 0..127
       const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
       int prow;  // weight row relative to d_pbase
@@ -122,7 +128,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
     }
 #pragma unroll
     for (int i = 0; i < DMA_Q; ++i) {
-      const int rb = 4 * i + w;
+      const int rb = WAVES * i + w;
       const int rr = 8 * rb + drow;
       const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
       d_voff[DMA_P + i] = (uint32_t)(min(rr, qmax) * a.ldq + lchunk * 16);
@@ -130,19 +136,24 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
     const int64_t prow0 = (EPI == EPI_SWIGLU) ? (int64_t)pt * 64 : (int64_t)pt * TP;
     d_pbase = (uint64_t)(a.p + (int64_t)ti.x * a.p_estride + prow0 * a.ldp);
     d_qbase = (uint64_t)(a.q + (int64_t)ti.y * a.ldq);
-    // token-row scales: wave w loads rows 64w + lane (clamped) of each k-block
-    d_sxbase = (uint64_t)(a.sx + ti.y);
-    d_sxoff = (uint32_t)(min(64 * w + l, qmax) * 4);
-    // weight-block scales: lane parity selects the gate / up block (SWIGLU)
-    const int64_t kb_n = a.kred / TKB;
-    int blk;
-    if constexpr (EPI == EPI_SWIGLU)
-      blk = (l & 1) ? (int)((a.hidden + (int64_t)pt * 64) / 128) : (pt * 64) / 128;
-    else
-      blk = pt;
-    d_swbase = (uint64_t)(a.sw + (int64_t)ti.x * a.sw_estride);
-    d_swoff = (uint32_t)(blk * kb_n * 4);
-    if constexpr (EPI == EPI_SCATTER) {
+    if (w < 4) {
+      // token-row scales: wave w loads rows 64w + lane (clamped) of each k-block
+      d_scbase = (uint64_t)(a.sx + ti.y);
+      d_scoff = (uint32_t)(min(64 * w + l, qmax) * 4);
+      d_scstep = (uint64_t)a.ldsx * 4;
+    } else {
+      // weight-block scales: lane parity selects the gate / up block (SWIGLU)
+      const int64_t kb_n = a.kred / TKB;
+      int blk;
+      if constexpr (EPI == EPI_SWIGLU)
+        blk = (l & 1) ? (int)((a.hidden + (int64_t)pt * 64) / 128) : (pt * 64) / 128;
+      else
+        blk = pt;
+      d_scbase = (uint64_t)(a.sw + (int64_t)ti.x * a.sw_estride);
+      d_scoff = (uint32_t)(blk * kb_n * 4);
+      d_scstep = 4;
+    }
+    if (EPI == EPI_SCATTER && w < 4) {
       const uint32_t q = (uint32_t)min(64 * w + l, qmax);
       const uint32_t m = lds0 + LDS_BYTES + (uint32_t)((r % META_SLOTS) * META_BYTES) + w * 256;
       if (a.dest) dma4(q * 4, (uint64_t)(a.dest + ti.y), m);
@@ -159,11 +170,10 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
     const uint64_t qb = d_qbase + (uint64_t)ks * TKB;
     const uint32_t st = lds0 + (uint32_t)((s % NSTAGE) * STAGE_BYTES);
 #pragma unroll
-    for (int i = 0; i < DMA_P; ++i) dma16(d_voff[i], pb, st + w * 1024 + i * 4096);
+    for (int i = 0; i < DMA_P; ++i) dma16(d_voff[i], pb, st + w * 1024 + i * (WAVES * 1024));
 #pragma unroll
-    for (int i = 0; i < DMA_Q; ++i) dma16(d_voff[DMA_P + i], qb, st + P_BYTES + w * 1024 + i * 4096);
-    dma4(d_sxoff, d_sxbase + (uint64_t)ks * a.ldsx * 4, st + SX_OFF + w * 256);
-    dma4(d_swoff, d_swbase + (uint64_t)ks * 4, st + SW_OFF + w * 256);
+    for (int i = 0; i < DMA_Q; ++i) dma16(d_voff[DMA_P + i], qb, st + P_BYTES + w * 1024 + i * (WAVES * 1024));
+    dma4(d_scoff, d_scbase + (uint64_t)ks * d_scstep, st + d_sclds);
   };
 
   // ---- fragment geometry -------------------------------------------------------
@@ -188,17 +198,17 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
     f.a[pb] = frag16(smem + (s % NSTAGE) * STAGE_BYTES, arow[pb]);
   };
   auto read_b = [&](Frag16& f, int s, int jb) {
-    f.b[jb] = frag16(smem + (s % NSTAGE) * STAGE_BYTES + P_BYTES, 128 * wq + 16 * jb);
+    f.b[jb] = frag16(smem + (s % NSTAGE) * STAGE_BYTES + P_BYTES, 64 * wq + 16 * jb);
   };
   float sxv[NJ16], swv[NPB16];
   auto read_scales = [&](int s) {
     const char* st = smem + (s % NSTAGE) * STAGE_BYTES;
 #pragma unroll
-    for (int jb = 0; jb < NJ16; ++jb) sxv[jb] = *(const float*)(st + SX_OFF + (128 * wq + 16 * jb + r16) * 4);
+    for (int jb = 0; jb < NJ16; ++jb) sxv[jb] = *(const float*)(st + SX_OFF + (64 * wq + 16 * jb + r16) * 4);
 #pragma unroll
     for (int pb = 0; pb < NPB16; ++pb) {
       const int lane = (EPI == EPI_SWIGLU) ? (pb >> 1) : 0;
-      swv[pb] = *(const float*)(st + SW_OFF + w * 256 + lane * 4);
+      swv[pb] = *(const float*)(st + SW_OFF + lane * 4);  // wave 4's copy
     }
   };
 
@@ -267,13 +277,13 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
       read_scales(s + 1);
     }
 
-    // ---- epilogue: acc[pb][jb][i] is (token row 128wq + 16jb + lane % 16,
+    // ---- epilogue: acc[pb][jb][i] is (token row 64wq + 16jb + lane % 16,
     //      weight row arow[pb] + 4 (lane / 16) + i).
     int er16 = r16;
     asm volatile("" : "+v"(er16));
 #pragma unroll
     for (int jb = 0; jb < NJ16; ++jb) {
-      const int gq = row0 + 128 * wq + 16 * jb + er16;
+      const int gq = row0 + 64 * wq + 16 * jb + er16;
       const bool row_ok = gq < row1;
       if constexpr (EPI == EPI_SWIGLU) {
         const bool clamp = (a.limit == a.limit);
@@ -308,7 +318,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
         int orow_idx = gq;
         if constexpr (EPI == EPI_SCATTER) {
           const int* meta = (const int*)(smem + LDS_BYTES + (r % META_SLOTS) * META_BYTES);
-          const int qrow = 128 * wq + 16 * jb + er16;
+          const int qrow = 64 * wq + 16 * jb + er16;
           if (a.dest) orow_idx = min(max(meta[qrow], 0), a.n_dest - 1);
           if (a.row_scale) scl = __int_as_float(meta[TQ + qrow]);
         }
