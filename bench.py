@@ -212,14 +212,20 @@ def main():
 
     # Stage breakdown (not part of the timed steps): event pairs around every
     # stage on the stream the kernels run on, averaged over extra forward
-    # passes (no-grad passes for the training configs).
+    # passes (no-grad passes for the training configs).  The passes are
+    # queued back to back with one synchronisation at the end, so that no
+    # pass starts on an idle GPU (the first stage's start event would then
+    # also time the host's launch of that stage).
     stage_us = {}
     n_stage = 20
+    passes = []
     for _ in range(n_stage):
         ev = {}
         with torch.no_grad():
             step_forward(ev)
-        torch.cuda.synchronize()
+        passes.append(ev)
+    torch.cuda.synchronize()
+    for ev in passes:
         for name, (s0, s1) in ev.items():
             stage_us[name] = stage_us.get(name, 0.0) + s0.elapsed_time(s1) * 1000.0 / n_stage
     log(f"stages (us): {json.dumps({k: round(v, 1) for k, v in stage_us.items()})}")
