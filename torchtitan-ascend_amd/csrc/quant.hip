@@ -101,8 +101,7 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint4* __restr
       float m = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(f[i]));
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+      m = row16_max(m);  // the block's 16 lanes are one DPP row
       const float s = m / 448.0f;
       const float rs = (s > 0.f) ? __builtin_amdgcn_rcpf(s) : 0.f;
       float q[8];

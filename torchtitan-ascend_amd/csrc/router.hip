@@ -161,38 +161,6 @@ struct RouterTopkArgs {
   bf16_t* logits;     // [T, E] or null
 };
 
-// All-reduce over the 16 lanes of a DPP row in four pairwise steps: xor 1,
-// xor 2 (quad permutes), then the half-row and row mirrors.  Each step
-// combines a lane with one partner and the pairs are symmetric, so with a
-// commutative combine every lane ends with bit-identical results.
-constexpr int kDppXor1 = 0xb1;        // quad_perm [1, 0, 3, 2]
-constexpr int kDppXor2 = 0x4e;        // quad_perm [2, 3, 0, 1]
-constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each 8
-constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within the row
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
-}
-
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp_f<kDppXor1>(v));
-  v = fmaxf(v, dpp_f<kDppXor2>(v));
-  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
-  return fmaxf(v, dpp_f<kDppMirror>(v));
-}
-
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp_f<kDppXor1>(v);
-  v += dpp_f<kDppXor2>(v);
-  v += dpp_f<kDppHalfMirror>(v);
-  return v + dpp_f<kDppMirror>(v);
-}
-
 // (selection value desc, expert id asc) winner, with its unbiased score.
 template <int CTRL>
 __device__ __forceinline__ void argmax_step(float& bv, int& bi, float& bs) {
