@@ -178,7 +178,8 @@ hipError_t launch_grouped_mm_fp8(const void* xq, const float* sx, const void* wq
                                  const int* offs, int M, int E, int N, int K, void* out, void* ws,
                                  hipStream_t stream) {
   Fp8Args a = fp8_args(xq, sx, wq, sw, M, N, K);
-  a.np_tiles = N / 128;
+  a.np_tiles = (N + 255) / 256;
+  a.n_p = N;
   a.out = (bf16_t*)out;
   a.ldo = N;
   return fp8(EPI_STORE, a, offs, E, M, ws, stream);
@@ -189,7 +190,8 @@ hipError_t launch_grouped_mm_fp8_swiglu(const void* xq, const float* sx, const v
                                         float limit, void* a_out, void* h_out, void* ws,
                                         hipStream_t stream) {
   Fp8Args a = fp8_args(xq, sx, w13q, s13, M, 2 * H, D);
-  a.np_tiles = H / 64;
+  a.np_tiles = (H + 127) / 128;  // 128 gate + 128 up rows per tile (H % 64 == 0)
+  a.n_p = 2 * H;
   a.out = (bf16_t*)a_out;
   a.ldo = H;
   a.hidden = H;
@@ -204,7 +206,8 @@ hipError_t launch_grouped_mm_fp8_unpermute(const void* aq, const float* sa, cons
                                            const float* row_scale, const int* dest, int n_dest,
                                            void* out, void* ws, hipStream_t stream) {
   Fp8Args a = fp8_args(aq, sa, w2q, s2, M, D, H);
-  a.np_tiles = D / 128;
+  a.np_tiles = (D + 255) / 256;
+  a.n_p = D;
   a.out = (bf16_t*)out;
   a.ldo = D;
   a.row_scale = row_scale;

@@ -141,6 +141,7 @@ struct Fp8Args {
   int64_t ldp;
   int kred;
   int np_tiles;  // weight-row tiles per token tile
+  int n_p;       // weight rows N (STORE, SCATTER: the last tile may hold only 128)
   const int4* table;
   const int* n_qtiles;
   const float* sx;  // activation scales [kred/128][ldsx] (k-block major)

@@ -11,27 +11,33 @@
 // sw [E, N/128, K/128].  The scales are the absmax / 448 recipe; the
 // reference semantics are "dequantise both operands, fp32 GEMM".
 //
-// Tile: up to 256 token rows (Q) x 128 weight rows (P); k in stages of 128
-// (one scale block, one 128-byte line per row).
-//   * 8 waves, two per SIMD, 4 x 2: wave (wq, wp) owns token rows 64wq.. and
-//     64 weight rows (SWIGLU: 32 gate rows and the 32 matching up rows), i.e.
-//     4 x 4 blocks of v_mfma_scale_f32_16x16x128_f8f6f4 (unit hardware
+// Tile: up to 256 token rows (Q) x 256 weight rows (P; SWIGLU: 128 gate rows
+// and the 128 matching up rows); k in stages of 128 (one scale block, one
+// 128-byte line per row).
+//   * 8 waves, two per SIMD, 2 x 4: wave (wq, wp) owns token rows 128wq..
+//     and 64 weight rows (SWIGLU: 32 gate rows and the 32 matching up rows),
+//     i.e. 4 x 8 blocks of v_mfma_scale_f32_16x16x128_f8f6f4 (unit hardware
 //     scales): one MFMA covers a block's whole k = 128 scale block, and its
 //     partial sum goes straight into the fp32 accumulator times sx * sw, so
 //     the fp32 block scales are applied once per block as in the dequantised
-//     form, with no partial sums kept across MFMAs.  The scale FMAs are VALU
-//     work of about half the MFMA time; with two waves per SIMD one wave's
-//     FMAs run under the other's MFMAs, and 64 accumulator registers per wave
-//     leave the partial sums in VGPRs (with one wave per SIMD and 128
-//     accumulators each FMA also needed an AGPR read).
-//   * Three LDS stages of 50 KB: 16 KB weight rows + 32 KB token rows (DMA,
+//     form, with no partial sums kept across MFMAs.  The scale FMAs of token
+//     block jb - 1 run under block jb's MFMAs, and with two waves per SIMD
+//     under the other wave's as well.
+//   * The kernel is bound by the L2 -> LDS stream (each CU keeps about 64
+//     line requests in flight), so the tile is as large as the registers
+//     allow: 256 x 256 moves 66 KB per 16.8 MFLOP stage where 256 x 128
+//     moved 48 KB per 8.4.  The 128 accumulators leave room for the 4
+//     weight fragments of the stage and only 2 token fragments, read just
+//     before use.
+//   * Two LDS stages of 66 KB: 32 KB weight rows + 32 KB token rows (DMA,
 //     global_load_lds_dwordx4, 8 rows per instruction, XOR-swizzled 16-byte
-//     chunks as in the bf16 kernel), 1 KB of token-row scales (waves 0-3) and
-//     the stage's weight-block scales (waves 4-7 each load a copy, so every
-//     wave issues the same DMA count; all read wave 4's).  The barrier at the
-//     top of stage s waits for stage s + 1, so while stage s is computed from
-//     registers, each fragment register is refilled with stage s + 1 right
-//     after its last use.
+//     chunks as in the bf16 kernel), 1 KB of token-row scales (waves 0-3)
+//     and the stage's weight-block scales (waves 4-7 each load a copy, so
+//     every wave issues the same DMA count; all read wave 4's).  At the top
+//     of stage s every wave waits for stage s (the only one in flight) and
+//     passes the barrier, which also means stage s - 1 has been read, and
+//     stage s + 1 is issued into its buffer: one stage ahead keeps the
+//     bounding DMA stream busy.
 //   * Persistent workgroups, XCD-aware slots, flattened (tile, stage) DMA
 //     stream and the EPI_SCATTER metadata in LDS follow gemm_fwd.hip.
 #include "common.h"
@@ -44,29 +50,27 @@ namespace {
 
 using namespace dma;
 
-constexpr int TQ = 256;  // token rows
-constexpr int TP = 128;  // weight rows
+constexpr int TQ = 256;   // token rows
+constexpr int TP = 256;   // weight rows (SWIGLU: 128 gate + the 128 matching up rows)
 constexpr int TKB = 128;  // k per stage (bytes per row)
-constexpr int NSTAGE = 3;
+constexpr int NSTAGE = 2;
 constexpr int WAVES = 8;
 constexpr int FTHREADS = 64 * WAVES;
-constexpr int P_BYTES = TP * TKB;  // 16 KB
+constexpr int P_BYTES = TP * TKB;  // 32 KB
 constexpr int Q_BYTES = TQ * TKB;  // 32 KB
 constexpr int SX_OFF = P_BYTES + Q_BYTES;
 constexpr int SW_OFF = SX_OFF + TQ * 4;
-constexpr int STAGE_BYTES = SW_OFF + 4 * 256;     // 50 KB
-constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;   // 150 KB
-constexpr int DMA_P = TP / 8 / WAVES;             // 2
+constexpr int STAGE_BYTES = SW_OFF + 4 * 256;     // 66 KB
+constexpr int LDS_BYTES = NSTAGE * STAGE_BYTES;   // 132 KB
+constexpr int DMA_P = TP / 8 / WAVES;             // 4
 constexpr int DMA_Q = TQ / 8 / WAVES;             // 4
-constexpr int DMA_PER_STAGE = DMA_P + DMA_Q + 1;  // + row scales (waves 0-3) or weight-block scales (4-7)
-static_assert(TQ == 4 * 64 && TP == 2 * 64 && WAVES == 8, "wave layout: 4 token x 2 weight quarters");
-// EPI_SCATTER metadata slots (tile round % 4): tile r's slot is written
-// when its first stage is issued, three stages ahead, so with one-stage
-// tiles (k = 128) the writer runs three rounds ahead of the epilogue that
-// last read the slot; four slots keep them apart for every k.
+static_assert(TQ == 2 * 128 && TP == 4 * 64 && WAVES == 8, "wave layout: 2 token halves x 4 weight quarters");
+// EPI_SCATTER metadata slots (tile round % 3): tile r's slot is written
+// when its first stage is issued, at the top of tile r - 1's last stage,
+// after every wave has passed tile r - 2's epilogue.
 constexpr int META_BYTES = TQ * 8;
-constexpr int META_SLOTS = 4;
-constexpr int LDS_TOTAL = LDS_BYTES + META_SLOTS * META_BYTES;  // 158 KB
+constexpr int META_SLOTS = 3;
+constexpr int LDS_TOTAL = LDS_BYTES + META_SLOTS * META_BYTES;  // 138 KB
 static_assert(LDS_TOTAL <= 160 * 1024, "LDS");
 
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
@@ -74,21 +78,19 @@ typedef int i32x8_t __attribute__((ext_vector_type(8)));
 // Chunk permutation of 128-byte LDS rows (as in gemm_fwd.hip).
 __device__ __forceinline__ int cswz(int r) { return (r ^ (r >> 3)) & 7; }
 
-// Fragments of one stage (k = 128): NPB16 weight blocks and NJ16 token
-// blocks of 16 rows; lane l holds bytes 32 (l / 16) .. + 31 of row l % 16.
+// A wave's blocks of 16 rows: NPB16 weight blocks (held for the stage) and
+// NJ16 token blocks (read just before use, NBS in registers at a time);
+// lane l holds bytes 32 (l / 16) .. + 31 of row l % 16.
 constexpr int NPB16 = 4;
-constexpr int NJ16 = 4;
-struct Frag16 {
-  i32x8_t a[NPB16];
-  i32x8_t b[NJ16];
-};
+constexpr int NJ16 = 8;
+constexpr int NBS = 2;
 
 template <int EPI>
 __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wq = w >> 1;
-  const int wp = w & 1;
+  const int wq = w >> 2;  // token half: rows 128 wq ..
+  const int wp = w & 3;   // weight quarter; waves w and w + 4 share a SIMD
   const int l = threadIdx.x & 63;
   const int G = gridDim.x;
   const int b = blockIdx.x;
@@ -105,8 +107,15 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
   // ---- DMA stream -----------------------------------------------------------
   int d_r = -1;
   uint64_t d_pbase = 0, d_qbase = 0, d_scbase = 0, d_scstep = 0;
-  uint32_t d_voff[DMA_P + DMA_Q];
+  int d_qmax = 0, d_pmax = 0, d_hmax = 0;
   uint32_t d_scoff = 0;
+  // DMA instruction i of wave w moves tile rows rr0 + 64 i (row block
+  // 8 i + w); its chunk permutation (drow ^ w) & 7 is the same for every i,
+  // so the per-lane offsets are recomputed at issue from rr0 and lch16
+  // instead of being held through the k loop.
+  static_assert(WAVES == 8, "row block 8 i + w has chunk permutation term w");
+  const int rr0 = 8 * w + drow;
+  const uint32_t lch16 = (uint32_t)(((l & 7) ^ ((drow ^ w) & 7)) * 16);
   const uint32_t d_sclds = (w < 4) ? (uint32_t)(SX_OFF + w * 256) : (uint32_t)(SW_OFF + (w - 4) * 256);
   auto dma_tile = [&](int r) {
     const int tile = r * G + slot;
@@ -114,26 +123,10 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
     const int pt = tile - qt * a.np_tiles;
     const int4 ti = sload_int4(a.table + qt);
     const int qmax = ti.z - ti.y - 1;
-#pragma unroll
-    for (int i = 0; i < DMA_P; ++i) {
-      const int rb = WAVES * i + w;
-      const int rr = 8 * rb + drow;  // tile weight row 0..127
-      const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
-      int prow;  // weight row relative to d_pbase
-      if constexpr (EPI == EPI_SWIGLU)
-        prow = (rr < 64) ? rr : (int)a.hidden + (rr - 64);
-      else
-        prow = rr;
-      d_voff[i] = (uint32_t)(prow * a.ldp + lchunk * 16);
-    }
-#pragma unroll
-    for (int i = 0; i < DMA_Q; ++i) {
-      const int rb = WAVES * i + w;
-      const int rr = 8 * rb + drow;
-      const int lchunk = (l & 7) ^ ((drow ^ rb) & 7);
-      d_voff[DMA_P + i] = (uint32_t)(min(rr, qmax) * a.ldq + lchunk * 16);
-    }
-    const int64_t prow0 = (EPI == EPI_SWIGLU) ? (int64_t)pt * 64 : (int64_t)pt * TP;
+    d_qmax = qmax;
+    d_pmax = a.n_p - 1 - pt * TP;  // last weight row of a partial tile (STORE, SCATTER)
+    d_hmax = (int)a.hidden - 1 - pt * 128;  // SWIGLU: last gate (and up) row of the tile
+    const int64_t prow0 = (EPI == EPI_SWIGLU) ? (int64_t)pt * 128 : (int64_t)pt * TP;
     d_pbase = (uint64_t)(a.p + (int64_t)ti.x * a.p_estride + prow0 * a.ldp);
     d_qbase = (uint64_t)(a.q + (int64_t)ti.y * a.ldq);
     if (w < 4) {
@@ -142,13 +135,18 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
       d_scoff = (uint32_t)(min(64 * w + l, qmax) * 4);
       d_scstep = (uint64_t)a.ldsx * 4;
     } else {
-      // weight-block scales: lane parity selects the gate / up block (SWIGLU)
+      // weight-block scales; every wave 4..7 loads a copy.  STORE, SCATTER:
+      // lane parity selects the tile's first or second 128-row block.
+      // SWIGLU: lane 0 the gate block (the tile's 128 gate rows start on a
+      // block), lane 1 + q the up block of weight quarter q (with H % 128 ==
+      // 64 the tile's up rows straddle two blocks; a quarter's 32 do not).
       const int64_t kb_n = a.kred / TKB;
       int blk;
       if constexpr (EPI == EPI_SWIGLU)
-        blk = (l & 1) ? (int)((a.hidden + (int64_t)pt * 64) / 128) : (pt * 64) / 128;
+        blk = (l == 0) ? pt : (int)((a.hidden + (int64_t)pt * 128 + 32 * min(l - 1, 3)) / 128);
       else
-        blk = pt;
+        blk = 2 * pt + (l & 1);
+      blk = min(blk, a.n_p / 128 - 1);
       d_scbase = (uint64_t)(a.sw + (int64_t)ti.x * a.sw_estride);
       d_scoff = (uint32_t)(blk * kb_n * 4);
       d_scstep = 4;
@@ -162,28 +160,35 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
     d_r = r;
   };
   auto issue = [&](int s) {
-    const int sc = min(s, total - 1);  // past the end: re-load the last stage
-    const int r = sc / ksteps;
-    const int ks = sc - r * ksteps;
+    const int r = s / ksteps;
+    const int ks = s - r * ksteps;
     if (r != d_r) dma_tile(r);
     const uint64_t pb = d_pbase + (uint64_t)ks * TKB;
     const uint64_t qb = d_qbase + (uint64_t)ks * TKB;
     const uint32_t st = lds0 + (uint32_t)((s % NSTAGE) * STAGE_BYTES);
 #pragma unroll
-    for (int i = 0; i < DMA_P; ++i) dma16(d_voff[i], pb, st + w * 1024 + i * (WAVES * 1024));
+    for (int i = 0; i < DMA_P; ++i) {
+      int prow;  // weight row relative to d_pbase
+      if constexpr (EPI == EPI_SWIGLU)
+        prow = (i < 2) ? min(rr0 + 64 * i, d_hmax) : (int)a.hidden + min(rr0 + 64 * (i - 2), d_hmax);
+      else
+        prow = min(rr0 + 64 * i, d_pmax);
+      dma16((uint32_t)(prow * a.ldp) + lch16, pb, st + w * 1024 + i * (WAVES * 1024));
+    }
 #pragma unroll
-    for (int i = 0; i < DMA_Q; ++i) dma16(d_voff[DMA_P + i], qb, st + P_BYTES + w * 1024 + i * (WAVES * 1024));
+    for (int i = 0; i < DMA_Q; ++i)
+      dma16((uint32_t)(min(rr0 + 64 * i, d_qmax) * a.ldq) + lch16, qb, st + P_BYTES + w * 1024 + i * (WAVES * 1024));
     dma4(d_scoff, d_scbase + (uint64_t)ks * d_scstep, st + d_sclds);
   };
 
   // ---- fragment geometry -------------------------------------------------------
   const int r16 = l & 15;
   const int g4 = l >> 4;
-  const int f16 = cswz(r16);  // cswz(16m + r16) = f16 ^ 2 (m & 3 ... see arow)
+  const int f16 = cswz(r16);
   int arow[NPB16];  // weight block starts (tile rows)
 #pragma unroll
   for (int pb = 0; pb < NPB16; ++pb)
-    arow[pb] = (EPI == EPI_SWIGLU) ? (pb < 2 ? 32 * wp + 16 * pb : 64 + 32 * wp + 16 * (pb - 2))
+    arow[pb] = (EPI == EPI_SWIGLU) ? (pb < 2 ? 32 * wp + 16 * pb : 128 + 32 * wp + 16 * (pb - 2))
                                    : 64 * wp + 16 * pb;
   // Row 16m + r16 of a 128-byte-row operand: cswz = f16 ^ ((2m) & 6) (16m >> 3
   // = 2m is even, so adding r16 >> 3 does not carry).
@@ -194,35 +199,11 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
     const i32x4_t hi = *(const i32x4_t*)(row + (((2 * g4 + 1) ^ x) * 16));
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   };
-  auto read_a = [&](Frag16& f, int s, int pb) {
-    f.a[pb] = frag16(smem + (s % NSTAGE) * STAGE_BYTES, arow[pb]);
-  };
-  auto read_b = [&](Frag16& f, int s, int jb) {
-    f.b[jb] = frag16(smem + (s % NSTAGE) * STAGE_BYTES + P_BYTES, 64 * wq + 16 * jb);
-  };
-  float sxv[NJ16], swv[NPB16];
-  auto read_scales = [&](int s) {
-    const char* st = smem + (s % NSTAGE) * STAGE_BYTES;
-#pragma unroll
-    for (int jb = 0; jb < NJ16; ++jb) sxv[jb] = *(const float*)(st + SX_OFF + (64 * wq + 16 * jb + r16) * 4);
-#pragma unroll
-    for (int pb = 0; pb < NPB16; ++pb) {
-      const int lane = (EPI == EPI_SWIGLU) ? (pb >> 1) : 0;
-      swv[pb] = *(const float*)(st + SW_OFF + lane * 4);  // wave 4's copy
-    }
-  };
+  // weight-block scale of block pb (the copy wave 4 loaded)
+  auto sw_lane = [&](int pb) { return (EPI == EPI_SWIGLU) ? (pb < 2 ? 0 : 1 + wp) : (wp >> 1); };
 
-  // ---- prologue: stages 0..2 issued; stages 0 and 1 landed; stage 0 read ----
+  // ---- prologue: stage 0 in flight ----------------------------------------------
   issue(0);
-  issue(1);
-  issue(2);
-  wait_vm_barrier<DMA_PER_STAGE>();
-  Frag16 f;
-#pragma unroll
-  for (int pb = 0; pb < NPB16; ++pb) read_a(f, 0, pb);
-#pragma unroll
-  for (int jb = 0; jb < NJ16; ++jb) read_b(f, 0, jb);
-  read_scales(0);
 
   int s = 0;
   for (int r = 0; r < nmy; ++r) {
@@ -241,56 +222,70 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
         for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
 
     for (int ks = 0; ks < ksteps; ++ks, ++s) {
-      // Every wave has read stage s (fragments and scales are in registers)
-      // and stage s + 1 has landed (only s + 2 may be in flight): stage s's
-      // buffer takes stage s + 3, and stage s + 1 is read as registers free.
-      wait_vm_barrier<DMA_PER_STAGE>();
-      issue(s + NSTAGE);
-      float sw_cur[NPB16];
+      // Stage s has landed (the only stage in flight) and every wave is done
+      // with stage s - 1: its buffer takes stage s + 1.  The DMA stream is
+      // the bound, so one stage ahead keeps it busy.
+      wait_vm_barrier<0>();
+      if (s + 1 < total) issue(s + 1);
+      const char* st = smem + (s % NSTAGE) * STAGE_BYTES;
+      i32x8_t fa[NPB16];
+      float swv[NPB16];
 #pragma unroll
-      for (int pb = 0; pb < NPB16; ++pb) sw_cur[pb] = swv[pb];
-      // The MFMAs of token block jb + 1 are issued before the scaled
-      // accumulation of block jb, so no FMA waits on an MFMA just issued.
-      floatx4_t part[2][NPB16];
-      auto mfma_block = [&](int jb, floatx4_t (&dst)[NPB16]) {
-#pragma unroll
-        for (int pb = 0; pb < NPB16; ++pb) {
-          floatx4_t z = {};
-          dst[pb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(f.a[pb], f.b[jb], z, 0, 0, 0, 127, 0, 127);
-        }
+      for (int pb = 0; pb < NPB16; ++pb) {
+        fa[pb] = frag16(st, arow[pb]);
+        swv[pb] = *(const float*)(st + SW_OFF + sw_lane(pb) * 4);
+      }
+      i32x8_t fb[NBS];
+      float sxv[NBS];
+      auto read_b = [&](int jb) {
+        const int row = 128 * wq + 16 * jb;
+        fb[jb % NBS] = frag16(st + P_BYTES, row);
+        sxv[jb % NBS] = *(const float*)(st + SX_OFF + (row + r16) * 4);
       };
-      mfma_block(0, part[0]);
-#pragma unroll
-      for (int jb = 0; jb < NJ16; ++jb) {
-        if (jb + 1 < NJ16) mfma_block(jb + 1, part[(jb + 1) & 1]);
-        read_b(f, s + 1, jb);
-        const float sxj = sxv[jb];
+      read_b(0);
+      read_b(1);
+      float sx_prev = 0.f;
+      floatx4_t part[2][NPB16];
+      auto scale_add = [&](int jb, float sxj) {
 #pragma unroll
         for (int pb = 0; pb < NPB16; ++pb) {
-          const float sc = sw_cur[pb] * sxj;
+          const float sc = swv[pb] * sxj;
 #pragma unroll
           for (int v = 0; v < 4; ++v) acc[pb][jb][v] += part[jb & 1][pb][v] * sc;
         }
-      }
+      };
 #pragma unroll
-      for (int pb = 0; pb < NPB16; ++pb) read_a(f, s + 1, pb);
-      read_scales(s + 1);
+      for (int jb = 0; jb < NJ16; ++jb) {
+#pragma unroll
+        for (int pb = 0; pb < NPB16; ++pb) {
+          floatx4_t z = {};
+          part[jb & 1][pb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fa[pb], fb[jb % NBS], z, 0, 0, 0, 127, 0, 127);
+        }
+        // block jb - 1's scale FMAs run under block jb's MFMAs; block jb's
+        // slot then takes block jb + 2, so its row scale is kept aside first
+        if (jb > 0) scale_add(jb - 1, sx_prev);
+        sx_prev = sxv[jb % NBS];
+        if (jb + 2 < NJ16) read_b(jb + 2);
+      }
+      scale_add(NJ16 - 1, sx_prev);
     }
 
-    // ---- epilogue: acc[pb][jb][i] is (token row 64wq + 16jb + lane % 16,
+    // ---- epilogue: acc[pb][jb][i] is (token row 128wq + 16jb + lane % 16,
     //      weight row arow[pb] + 4 (lane / 16) + i).
     int er16 = r16;
     asm volatile("" : "+v"(er16));
 #pragma unroll
     for (int jb = 0; jb < NJ16; ++jb) {
-      const int gq = row0 + 64 * wq + 16 * jb + er16;
+      const int gq = row0 + 128 * wq + 16 * jb + er16;
       const bool row_ok = gq < row1;
       if constexpr (EPI == EPI_SWIGLU) {
         const bool clamp = (a.limit == a.limit);
         const float L = a.limit;
+        // wave-uniform: this quarter's 32 gate columns lie past H (H % 128 == 64)
+        if (pt * 128 + 32 * wp >= a.hidden) continue;
 #pragma unroll
         for (int pb = 0; pb < 2; ++pb) {
-          const int col = pt * 64 + arow[pb] + 4 * g4;
+          const int col = pt * 128 + arow[pb] + 4 * g4;
           float av[4], gv[4], uv[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -313,12 +308,12 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
             }
           }
         }
-      } else {
+      } else if (pt * TP + 64 * wp < a.n_p) {  // wave-uniform: this quarter holds rows of N
         float scl = 1.f;
         int orow_idx = gq;
         if constexpr (EPI == EPI_SCATTER) {
           const int* meta = (const int*)(smem + LDS_BYTES + (r % META_SLOTS) * META_BYTES);
-          const int qrow = 64 * wq + 16 * jb + er16;
+          const int qrow = 128 * wq + 16 * jb + er16;
           if (a.dest) orow_idx = min(max(meta[qrow], 0), a.n_dest - 1);
           if (a.row_scale) scl = __int_as_float(meta[TQ + qrow]);
         }
@@ -334,7 +329,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  wait_vm<0>();  // DMAs past the end have landed before the workgroup exits
+  wait_vm<0>();  // DMAs have landed before the workgroup exits
 }
 
 template <int EPI>
