@@ -10,7 +10,8 @@ GEMM w2 + score + un-permute -> K-way sum, on inputs already resident in HBM.
 Prints ONE JSON line (bench contract) with `roofline` for the dominant
 kernel (the w13 grouped GEMM, timed in every timed step by an event pair the
 library records on the kernel's stream immediately around it) and
-`cpu_baseline` (the CPU oracle on a bounded sample of the workload).
+`cpu_baseline` (the reference op sequence restated in torch, timed on this
+host's CPU cores on a bounded sample of the workload).
 
 Other configs (--config c1|c3|c4|c5) are for development runs.
 """
@@ -51,16 +52,17 @@ CONFIGS = {
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # The GPU needs a few hundred ms of load to reach its steady clocks: 300
-    # warmup steps of C2 (~0.25 s) take the timed steps from ~0.85 to ~0.81 ms.
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device copy (reference for the PMC byte counters) and exit")
-    ap.add_argument("--cpu-tokens", type=int, default=2048, help="unused (kept for old command lines)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum CPU time of the oracle baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="about how much CPU time the reference-CPU baseline's timed runs take")
+    ap.add_argument("--settle-ms", type=float, default=400.0,
+                    help="untimed steps run for this long before the warm-up steps, so that the GPU's clocks "
+                         "have reached their steady state under this load")
     return ap.parse_args()
 
 
@@ -182,10 +184,22 @@ def main():
             with torch.no_grad():
                 return step_forward(ev)
 
+    # Clock settling (untimed, before the W warm-up steps): the GPU raises
+    # its clocks only after a few hundred ms of sustained load, so a run
+    # with few warm-up steps would otherwise time the ramp (C2: ~0.82 ms per
+    # step after 5 steps against ~0.77 at steady clocks).  Steps are queued
+    # in batches until --settle-ms of wall time has passed.
+    settle_steps = 0
+    t_settle = time.perf_counter()
+    while (time.perf_counter() - t_settle) * 1e3 < args.settle_ms:
+        for _ in range(10):
+            step()
+        settle_steps += 10
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    log("warmup done")
+    log(f"clock settling: {settle_steps} steps; warmup: {args.warmup} steps")
     # Timed region: K steps between two synchronisations, nothing else on the
     # stream but the roofline probe: the step's first forward grouped GEMM
     # (w13) is timed by the library, which records an event pair on the
@@ -258,6 +272,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_settle": {"ms": args.settle_ms, "steps": settle_steps},
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -289,21 +304,10 @@ def main():
         },
     }
 
-    if not fp8:
-        # The bf16 MFMA rate this GPU sustains on random operands (the GEMM's
-        # k loop alone, no memory traffic): the practical ceiling for
-        # `roofline.achieved`, measured after the timed region.
-        ceiling = ops.mfma_loop_ceiling(dev)
-        result["mfma_loop_ceiling"] = {
-            "tflops": round(ceiling, 1),
-            "frac_of_peak": round(ceiling / peak, 4),
-            "roofline_achieved_frac_of_ceiling": round(result["roofline"]["achieved"] / ceiling, 4),
-            "probe": "ttamd_probe_mfma_loop: gg_fwd k loop (LDS fragment reads + v_mfma_f32_32x32x16_bf16 + "
-                     "stage barriers) on pseudo-random bf16 data, no global memory traffic",
-        }
-        log(f"mfma loop ceiling on random data: {ceiling:.1f} TFLOP/s")
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args, cfg, x, w13, w2, router)
+        result["cpu_baseline"] = cpu_baseline(args, cfg, x, w13, w2, w_router, zipf_idx,
+                                              zipf_scores if zipf_idx is not None else None,
+                                              (sw13, sw2) if shared else None)
     print(json.dumps(result), flush=True)
 
 
@@ -351,52 +355,80 @@ def measured_traffic(config):
     return None
 
 
-def cpu_baseline(args, cfg, x, w13, w2, router):
-    """The CPU oracle (numpy restatement of the reference path) on a token sample."""
+def cpu_baseline(args, cfg, x, w13, w2, w_router, zipf_idx, zipf_scores, shared_w):
+    """The reference path's own op sequence (oracle/reference_cpu.py: torch
+    router, stable argsort + index_select, torch._grouped_mm bf16 for w13
+    and w2, silu(gate) * up, scatter + K-way sum) timed on this host's
+    cores: torch.set_num_threads(all cores we may use), one warm-up run, then
+    the median of >= 3 runs on a token sample sized to about
+    --cpu-seconds of work (the whole workload when that fits)."""
+    import subprocess
+
     import numpy as np
     import torch
 
-    from oracle import moe_oracle as O
+    from oracle import reference_cpu as R
 
+    cores = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS")
+    if share and share.isdigit() and 0 < int(share) < cores:
+        cores = int(share)  # the CPU share this process is given on the GPU box
+    torch.set_num_threads(cores)
+    model = "unknown"
     try:
-        from threadpoolctl import threadpool_info
+        out = subprocess.run(["lscpu"], stdout=subprocess.PIPE, stderr=subprocess.DEVNULL, text=True, timeout=10).stdout
+        model = [ln.split(":", 1)[1].strip() for ln in out.splitlines() if ln.startswith("Model name")][0]
+    except Exception:  # pragma: no cover
+        pass
+    T, E, K = cfg["T"], cfg["E"], cfg["K"]
+    xc = x.cpu()
+    w13c, w2c = w13.cpu(), w2.cpu()
+    wrc = w_router.cpu()
+    shared_c = None if shared_w is None else (shared_w[0].detach().cpu(), shared_w[1].detach().cpu())
+    lab = None if zipf_idx is None else zipf_idx.cpu()
+    lsc = None if zipf_scores is None else zipf_scores.cpu()
 
-        threads = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"), default=1)
-    except Exception:  # pragma: no cover
-        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
-    Tfull = cfg["T"]
-    with torch.no_grad():
-        scores, idx = router()
-    xs_all = x.float().cpu().numpy()
-    ss_all = scores.float().cpu().numpy()
-    ix_all = idx.cpu().numpy()
-    w13n = w13.float().cpu().numpy()
-    w2n = w2.float().cpu().numpy()
-    # warm-up on a small slice, then whole-workload passes until >= cpu_seconds
-    O.moe_forward(xs_all[:256], ss_all[:256], ix_all[:256], w13n, w2n, cfg["E"], cfg["score_before"])
-    log(f"cpu baseline: oracle forward on {Tfull} tokens per pass, {threads} BLAS threads")
-    t0 = time.perf_counter()
-    passes = 0
-    while True:
-        O.moe_forward(xs_all, ss_all, ix_all, w13n, w2n, cfg["E"], cfg["score_before"])
-        passes += 1
-        dt = time.perf_counter() - t0
-        if dt >= args.cpu_seconds or passes >= 50:
-            break
-    Ts = Tfull * passes
-    try:
-        model = [ln.split(":", 1)[1].strip() for ln in open("/proc/cpuinfo") if ln.startswith("model name")][0]
-    except Exception:  # pragma: no cover
-        model = "unknown"
+    def run(n):
+        xs = xc[:n]
+        if cfg["backward"]:
+            xs = xs.clone().requires_grad_(True)
+            w13r, w2r = w13c.clone().requires_grad_(True), w2c.clone().requires_grad_(True)
+            wrr = wrc.clone().requires_grad_(True)
+            sh = None if shared_c is None else tuple(t.clone().requires_grad_(True) for t in shared_c)
+        else:
+            w13r, w2r, wrr, sh = w13c, w2c, wrc, shared_c
+        t0 = time.perf_counter()
+        with torch.set_grad_enabled(cfg["backward"]):
+            out = R.moe_step(xs, wrr, w13r, w2r, E, K, cfg["router"], cfg["norm"], cfg["score_before"],
+                             labels=None if lab is None else lab[:n], label_scores=None if lsc is None else lsc[:n],
+                             shared=sh)
+            if cfg["backward"]:
+                out.backward(torch.ones_like(out))
+        return time.perf_counter() - t0
+
+    # size the sample from one small probe run, then warm up once on it
+    n0 = min(T, 512)
+    dt0 = max(run(n0), 1e-3)
+    n = int(min(T, max(n0, n0 * args.cpu_seconds / 3.0 / dt0)))
+    n = max(K, n - n % 8)
+    log(f"cpu baseline: reference op sequence (torch CPU) on {n} of {T} tokens, {cores} threads, {model}")
+    run(n)  # warm-up
+    reps = 3 if not cfg["backward"] else 1
+    times = sorted(run(n) for _ in range(reps))
+    med = float(np.median(times))
+    kind = "fwd+bwd" if cfg["backward"] else "forward"
     return {
-        "value": round(Ts / dt, 1),
-        "unit": "tokens/s",
-        "cores": threads,
+        "value": round(n / med, 1),
+        "unit": "tokens/s" if cfg["router"] != "zipf" else "pairs/s",
+        "cores": cores,
         "kind": "port",
-        "sample": f"{passes} pass(es) of the full workload forward ({Tfull} tokens each, same inputs and routing) "
-                  f"through oracle.moe_oracle.moe_forward (numpy fp32): {dt:.2f} s on {model}",
+        "sample": f"{n} of the workload's {T} tokens (same inputs and routing), one {kind} of the reference op "
+                  f"sequence restated in torch on the CPU (oracle/reference_cpu.py: router F.linear bf16 + fp32 "
+                  f"{cfg['router']} + topk, histc + stable argsort + index_select, torch._grouped_mm bf16 w13 / w2, "
+                  f"silu(gate)*up, scatter + K-way sum{', shared expert' if shared_c is not None else ''}): "
+                  f"1 warm-up, median of {reps} runs = {med:.3f} s (runs {', '.join(f'{t:.3f}' for t in times)}); "
+                  f"torch.set_num_threads({cores}); CPU {model}",
     }
-
 
 if __name__ == "__main__":
     main()

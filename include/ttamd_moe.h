@@ -316,7 +316,8 @@ int ttamd_moe_sum_topk(const void* in, int64_t num_tokens, int64_t hidden,
  * a_scratch bf16 [T, H] is caller-owned scratch (the SwiGLU output).
  * x bf16 [T, D]; w13_shared [2H, D]; w2_shared [D, H]; D % 128 == 0,
  * H % 64 == 0; workspace: ttamd_gemm_workspace_bytes(T, 1).
- * swiglu_limit: <= 0 or NaN = no clamp.
+ * swiglu_limit: NaN = no clamp (the reference's swiglu_limit=None), else
+ * >= 0 (0 clamps to zero, as ttamd_grouped_mm_swiglu does).
  */
 int ttamd_shared_expert_add(const void* x, int64_t num_tokens, int64_t dim,
                             int64_t hidden, const void* w13_shared,
@@ -453,17 +454,6 @@ int ttamd_grouped_mm_fp8_unpermute(const void* aq, const float* sa_t,
  * NULL for both disarms.  Not thread-safe: one arming thread per process.
  */
 int ttamd_probe_next_gemm(void* start_event, void* end_event);
-
-/*
- * MFMA ceiling probe: launches, on `stream`, the forward grouped GEMM's k
- * loop with everything but the LDS fragment reads, the MFMAs and the stage
- * barriers taken out, on pseudo-random bf16 data held in LDS (one
- * workgroup per CU, `stages` 64-wide k stages each).  *flops receives the
- * launch's flop count; time it with events to get the bf16 MFMA rate the GPU
- * sustains on random operands (its power management lowers the clock for
- * them).  sink: 4 bytes of device memory (never written in practice).
- */
-int ttamd_probe_mfma_loop(int64_t stages, double* flops, void* sink, void* stream);
 
 #ifdef __cplusplus
 }

@@ -36,6 +36,11 @@ PINNED = {
                          "sigmoid(shared_expert_gate), expert_output + shared, model.py:794-809); a dropped gate "
                          "fails it",
     "moe_backward": "torch autograd of a torch fp32 restatement (golden); central finite differences",
+    "grouped_dgrad / grouped_wgrad": "through moe_backward's autograd golden (they are its dx / dW steps); "
+                                     "brute-force triple loop on tiny shapes",
+    "swiglu_backward": "through moe_backward (above); finite differences of swiglu on clamped and unclamped values",
+    "expert_weight_grad_slices": "equal to the matching slices of moe_backward's full dw13 / dw2 on small shapes "
+                                 "(a swapped gate/up half or a transposed slice fails it)",
     "bf16_round": "torch .to(bfloat16) on random and special values",
     "f32_to_e4m3_bits / e4m3_bits_to_f32": "torch .to(float8_e4m3fn) on every bf16 bit pattern, ties and edge "
                                           "values; the 256-entry decode table vs torch float8 -> float",
@@ -228,6 +233,36 @@ def grouped_mm(x: np.ndarray, w: np.ndarray, offs: np.ndarray) -> np.ndarray:
     return out
 
 
+def grouped_dgrad(dy: np.ndarray, w: np.ndarray, offs: np.ndarray) -> np.ndarray:
+    """Backward of grouped_mm w.r.t. x (autograd of torch._grouped_mm,
+    npu_gmm.py:31, :38): dx[m] = dy[m] @ w[e(m)], w [E, N, K]; fp32
+    accumulate; rows past offs[-1] are zero."""
+    dy = np.asarray(dy, np.float32)
+    w = np.asarray(w, np.float32)
+    dx = np.zeros((dy.shape[0], w.shape[2]), np.float32)
+    start = 0
+    for e, end in enumerate(np.asarray(offs).tolist()):
+        if end > start:
+            dx[start:end] = dy[start:end] @ w[e]
+        start = end
+    return dx
+
+
+def grouped_wgrad(dy: np.ndarray, x: np.ndarray, offs: np.ndarray, num_experts: int) -> np.ndarray:
+    """Backward of grouped_mm w.r.t. the weight: dw[e] = dy_e^T @ x_e over
+    expert e's rows [offs[e-1], offs[e]); an expert without rows gets exact
+    zeros.  dy [M, N], x [M, K] -> dw [E, N, K], fp32 accumulate."""
+    dy = np.asarray(dy, np.float32)
+    x = np.asarray(x, np.float32)
+    dw = np.zeros((num_experts, dy.shape[1], x.shape[1]), np.float32)
+    start = 0
+    for e, end in enumerate(np.asarray(offs).tolist()):
+        if end > start:
+            dw[e] = dy[start:end].T @ x[start:end]
+        start = end
+    return dw
+
+
 def swiglu(h: np.ndarray, swiglu_limit: float | None = None) -> np.ndarray:
     """Clamp (npu_gmm.py:32-36) then npu_swiglu (npu_gmm.py:37):
     gate = first half, up = second half; silu(gate) * up."""
@@ -340,16 +375,34 @@ def moe_backward(x, top_scores, idx, w13, w2, num_experts, score_before_experts,
     else:
         dy = g_tok * s_flat[sidx][:, None]
         dscores[sidx] = np.einsum("jd,jd->j", g_tok.astype(np.float64), y.astype(np.float64))
-    dw2 = np.zeros_like(np.asarray(w2, np.float32))
-    dw13 = np.zeros_like(np.asarray(w13, np.float32))
-    da = np.zeros_like(a)
-    start = 0
-    for e, end in enumerate(offs.tolist()):
-        if end > start:
-            dw2[e] = dy[start:end].T @ a[start:end]
-            da[start:end] = dy[start:end] @ np.asarray(w2[e], np.float32)
-        start = end
-    gate, up = h[:, :H], h[:, H:]
+    dw2 = grouped_wgrad(dy, a, offs, E)
+    da = grouped_dgrad(dy, w2, offs)
+    dh = swiglu_backward(da, h, swiglu_limit)
+    dw13 = grouped_wgrad(dh, routed, offs, E)
+    d_routed = grouped_dgrad(dh, w13, offs)
+    dx = np.zeros_like(x)
+    # sum_d |a_d b_d| of each score gradient's dot product <a, b>: the scale
+    # its rounding error is bounded by (tests compare per element against it)
+    dscores_abs = np.zeros(T * K, np.float32)
+    if score_before_experts:
+        dscores[sidx] = np.einsum("jd,jd->j", d_routed.astype(np.float64), xr.astype(np.float64))
+        dscores_abs[sidx] = np.einsum("jd,jd->j", np.abs(d_routed).astype(np.float64), np.abs(xr).astype(np.float64))
+        np.add.at(dx, tok, d_routed * s_flat[sidx][:, None])
+    else:
+        dscores_abs[sidx] = np.einsum("jd,jd->j", np.abs(g_tok).astype(np.float64), np.abs(y).astype(np.float64))
+        np.add.at(dx, tok, d_routed)
+    return {"dx": dx, "dscores": dscores.reshape(T, K), "dscores_abs": dscores_abs.reshape(T, K),
+            "dw13": dw13, "dw2": dw2}
+
+
+def swiglu_backward(da: np.ndarray, h: np.ndarray, swiglu_limit: float | None = None) -> np.ndarray:
+    """Gradient of swiglu(clamp(h)) (npu_gmm.py:32-37) w.r.t. the
+    pre-activation h = [gate | up], given da = d(activation): the clamp masks
+    come from h itself (torch.clamp's gradient is zero where it clamps).
+    Returns dh [.., 2H] = [da * up_c * silu'(gate_c) * [gate <= L],
+    da * silu(gate_c) * [-L <= up <= L]]."""
+    H = h.shape[-1] // 2
+    gate, up = h[..., :H], h[..., H:]
     gc, uc = gate, up
     mg = np.ones_like(gate)
     mu = np.ones_like(up)
@@ -360,21 +413,41 @@ def moe_backward(x, top_scores, idx, w13, w2, num_experts, score_before_experts,
         uc = np.clip(up, -swiglu_limit, swiglu_limit)
     sig = (1.0 / (1.0 + np.exp(-gc.astype(np.float64)))).astype(np.float32)
     dsilu = sig * (1.0 + gc * (1.0 - sig))
-    dh = np.concatenate([da * uc * dsilu * mg, da * gc * sig * mu], axis=1).astype(np.float32)
-    d_routed = np.zeros_like(routed)
-    start = 0
-    for e, end in enumerate(offs.tolist()):
-        if end > start:
-            dw13[e] = dh[start:end].T @ routed[start:end]
-            d_routed[start:end] = dh[start:end] @ np.asarray(w13[e], np.float32)
-        start = end
-    dx = np.zeros_like(x)
-    if score_before_experts:
-        dscores[sidx] = np.einsum("jd,jd->j", d_routed.astype(np.float64), xr.astype(np.float64))
-        np.add.at(dx, tok, d_routed * s_flat[sidx][:, None])
-    else:
-        np.add.at(dx, tok, d_routed)
-    return {"dx": dx, "dscores": dscores.reshape(T, K), "dw13": dw13, "dw2": dw2}
+    return np.concatenate([da * uc * dsilu * mg, da * gc * sig * mu], axis=-1).astype(np.float32)
+
+
+def expert_weight_grad_slices(routed: np.ndarray, dy: np.ndarray, w13_e: np.ndarray, w2_e: np.ndarray,
+                              gate_rows: np.ndarray, down_cols: np.ndarray, swiglu_limit: float | None = None,
+                              round_intermediates: bool = True):
+    """Selected slices of ONE expert's weight gradients under
+    _run_experts_grouped_mm's autograd (npu_gmm.py:31-38), without forming
+    the whole [2H, D] / [D, H] gradients: the gradient of gate row n needs
+    only columns n and H + n of the pre-activation, and column p of dW2 only
+    column p of the activation.
+      routed [n, D]: the expert's dispatched rows; dy [n, D]: gradient of
+      its output rows; w13_e [2H, D]; w2_e [D, H].
+    Returns (dw13_gate [len(gate_rows), D] = dW13[gate_rows],
+             dw13_up [len(gate_rows), D] = dW13[H + gate_rows],
+             dw2_cols [D, len(down_cols)] = dW2[:, down_cols]),
+    with the bf16 roundings of moe_backward(round_intermediates=...)."""
+    rnd = bf16_round if round_intermediates else (lambda v: v)
+    r = np.asarray(routed, np.float32)
+    g = np.asarray(dy, np.float32)
+    w13_e = np.asarray(w13_e, np.float32)
+    w2_e = np.asarray(w2_e, np.float32)
+    H = w2_e.shape[1]
+    gate_rows = np.asarray(gate_rows, np.int64)
+    down_cols = np.asarray(down_cols, np.int64)
+    h_sel = rnd(np.concatenate([r @ w13_e[gate_rows].T, r @ w13_e[H + gate_rows].T], axis=1))
+    da_sel = g @ w2_e[:, gate_rows]
+    dh_sel = swiglu_backward(da_sel, h_sel, swiglu_limit)
+    ng = gate_rows.size
+    dw13_gate = dh_sel[:, :ng].T @ r
+    dw13_up = dh_sel[:, ng:].T @ r
+    h_p = rnd(np.concatenate([r @ w13_e[down_cols].T, r @ w13_e[H + down_cols].T], axis=1))
+    a_p = rnd(swiglu(h_p, swiglu_limit))
+    dw2_cols = g.T @ a_p
+    return dw13_gate.astype(np.float32), dw13_up.astype(np.float32), dw2_cols.astype(np.float32)
 
 
 # ---------------------------------------------------------------------------

@@ -184,6 +184,45 @@ def test_regroup_permute_matches_reference_semantics(pkg):
     np.testing.assert_array_equal(to_np(back), x)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_regroup_permute_autograd(pkg, dtype):
+    """_permute is differentiable (torch_npu.npu_moe_token_permute is): the
+    gradient of routed_input is the permuted-row gradient scattered back,
+    grad[sorted[j]] = g[j] (oracle: inverse of the regroup order).  Rows move
+    bit for bit in the input's dtype, fp32 included; _unpermute's backward is
+    the matching gather."""
+    rng = np.random.default_rng(13)
+    ep, E_loc, D = 2, 6, 128
+    counts_group = rng.integers(0, 30, ep * E_loc)
+    counts_group[4] = 0
+    M = int(counts_group.sum()) + 3  # 3 rows past the grouped ones (label E_loc, sorted last)
+    x = (rng.standard_normal((M, D)) * 3).astype(np.float32)
+    if dtype == torch.bfloat16:
+        x = O.bf16_round(x)
+    disp = pkg.HipTokenDispatcher.Config(num_experts=E_loc * ep, top_k=1).build()
+    xd = torch.from_numpy(x).to(DEV).to(dtype).requires_grad_(True)
+    announce(f"regroup permute autograd {dtype}")
+    shape, permuted, pidx, _ = disp._permute(xd, torch.from_numpy(counts_group).to(DEV), ep, E_loc)
+    assert permuted.dtype == dtype and permuted.grad_fn is not None
+    _, ref_s, _ = O.regroup_permute(x, counts_group, ep, E_loc)
+    np.testing.assert_array_equal(pidx.cpu().numpy(), ref_s)
+    np.testing.assert_array_equal(permuted.detach().cpu().numpy(), x[ref_s])
+    g = (rng.standard_normal((M, D))).astype(np.float32)
+    permuted.backward(torch.from_numpy(g).to(DEV).to(dtype))
+    ref_grad = np.empty_like(g)
+    ref_grad[ref_s] = g
+    want = torch.from_numpy(ref_grad).to(dtype).float().numpy()
+    np.testing.assert_array_equal(xd.grad.float().cpu().numpy(), want)
+    # _unpermute(_permute(x)) == x bit for bit, and its backward gathers
+    y = permuted.detach().requires_grad_(True)
+    back = disp._unpermute(y, shape, pidx)
+    assert back.dtype == dtype
+    np.testing.assert_array_equal(back.detach().cpu().numpy(), xd.detach().cpu().numpy())
+    back.backward(torch.from_numpy(g).to(DEV).to(dtype))
+    np.testing.assert_array_equal(y.grad.float().cpu().numpy(),
+                                  torch.from_numpy(g).to(dtype).float().numpy()[ref_s])
+
+
 def test_group_labels_golden(ops):
     g = load_golden("regroup_labels")
     announce("group labels golden")

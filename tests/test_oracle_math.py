@@ -184,3 +184,96 @@ def test_planted_missing_score_is_caught():
     out = O.moe_forward(g["x"], np.ones_like(g["scores"]), g["idx"], g["w13"], g["w2"], int(g["num_experts"]),
                         False, None, round_intermediates=False)
     assert O.max_rel_err(out, g["out"]) > 0.1
+
+
+@pytest.mark.parametrize("limit", [None, 0.3])
+def test_expert_weight_grad_slices_match_full_backward(limit):
+    """The slice form equals the matching rows / columns of moe_backward's
+    full per-expert gradients (a swapped gate/up half, a transposed slice or
+    a dropped clamp mask fails it)."""
+    rng = np.random.default_rng(21)
+    T, E, D, H = 40, 3, 16, 12
+    x = O.bf16_round(rng.standard_normal((T, D)).astype(np.float32))
+    w13 = O.bf16_round((rng.standard_normal((E, 2 * H, D)) * 0.4).astype(np.float32))
+    w2 = O.bf16_round((rng.standard_normal((E, D, H)) * 0.4).astype(np.float32))
+    idx = rng.integers(0, E, (T, 1))
+    sc = (rng.random((T, 1)) * 0.8 + 0.2).astype(np.float32)
+    dout = rng.standard_normal((T, D)).astype(np.float32)
+    for before in (True, False):
+        full = O.moe_backward(x, sc, idx, w13, w2, E, before, dout, limit, round_intermediates=True)
+        for e in range(E):
+            rows = np.nonzero(idx[:, 0] == e)[0]  # stable order of one expert's tokens
+            routed = x[rows]
+            if before:
+                routed = O.bf16_round(routed * sc[rows])
+                dy = dout[rows]
+            else:
+                dy = dout[rows] * sc[rows]
+            gr, dc = np.array([0, 5, H - 1]), np.array([1, H - 2])
+            g13, u13, c2 = O.expert_weight_grad_slices(routed, dy, w13[e], w2[e], gr, dc, limit)
+            np.testing.assert_allclose(g13, full["dw13"][e][gr], rtol=1e-5, atol=1e-6)
+            np.testing.assert_allclose(u13, full["dw13"][e][H + gr], rtol=1e-5, atol=1e-6)
+            np.testing.assert_allclose(c2, full["dw2"][e][:, dc], rtol=1e-5, atol=1e-6)
+
+
+def test_swiglu_backward_finite_differences():
+    rng = np.random.default_rng(22)
+    H, L = 6, 0.7
+    h = (rng.standard_normal((5, 2 * H)) * 1.5).astype(np.float64)
+    da = rng.standard_normal((5, H))
+    for limit in (None, L):
+        dh = O.swiglu_backward(da.astype(np.float32), h.astype(np.float32), limit).astype(np.float64)
+        eps = 1e-4
+
+        def f(hh):
+            gate, up = hh[:, :H], hh[:, H:]
+            if limit is not None:
+                up, gate = np.clip(up, -limit, limit), np.minimum(gate, limit)
+            return (gate / (1 + np.exp(-gate)) * up * da).sum()
+        for (r, c) in ((0, 0), (2, 3), (4, H + 1), (1, H + 5)):
+            if limit is not None and abs(abs(h[r, c]) - limit) < 1e-3:
+                continue  # at the kink
+            hp, hm = h.copy(), h.copy()
+            hp[r, c] += eps
+            hm[r, c] -= eps
+            fd = (f(hp) - f(hm)) / (2 * eps)
+            assert abs(fd - dh[r, c]) < 1e-3 * max(1.0, abs(fd)), (limit, r, c)
+
+
+def test_dscores_abs_bounds_dscores():
+    """The dot-product scale returned with dscores bounds it: |<a,b>| <= sum|a b|."""
+    rng = np.random.default_rng(23)
+    T, K, E, D, H = 30, 2, 4, 16, 8
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    w13 = (rng.standard_normal((E, 2 * H, D)) * 0.3).astype(np.float32)
+    w2 = (rng.standard_normal((E, D, H)) * 0.3).astype(np.float32)
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(T)])
+    sc = rng.random((T, K)).astype(np.float32)
+    dout = rng.standard_normal((T, D)).astype(np.float32)
+    for before in (True, False):
+        g = O.moe_backward(x, sc, idx, w13, w2, E, before, dout)
+        assert (np.abs(g["dscores"]) <= g["dscores_abs"] * (1 + 1e-5)).all()
+        assert (g["dscores_abs"] > 0).all()
+
+
+def test_grouped_dgrad_wgrad_brute_force():
+    rng = np.random.default_rng(24)
+    M, E, N, K = 9, 4, 5, 3
+    counts = np.array([3, 0, 4, 1])  # one empty expert, one row past the last offset
+    offs = np.cumsum(counts)
+    dy = rng.standard_normal((M, N)).astype(np.float32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = rng.standard_normal((E, N, K)).astype(np.float32)
+    dx = O.grouped_dgrad(dy, w, offs)
+    dw = O.grouped_wgrad(dy, x, offs, E)
+    e_of = np.searchsorted(offs, np.arange(M), side="right")
+    for m in range(M):
+        for k in range(K):
+            want = sum(float(dy[m, n]) * float(w[e_of[m], n, k]) for n in range(N)) if m < offs[-1] else 0.0
+            assert abs(dx[m, k] - want) < 1e-5
+    for e in range(E):
+        for n in range(N):
+            for k in range(K):
+                want = sum(float(dy[m, n]) * float(x[m, k]) for m in range(M) if m < offs[-1] and e_of[m] == e)
+                assert abs(dw[e, n, k] - want) < 1e-5
+    assert not dw[1].any()

@@ -357,14 +357,6 @@ int ttamd_probe_next_gemm(void* start_event, void* end_event) {
   return 0;
 }
 
-int ttamd_probe_mfma_loop(int64_t stages, double* flops, void* sink, void* stream) {
-  const char* fn = "ttamd_probe_mfma_loop";
-  REQUIRE(stages >= 1 && stages <= (1LL << 24), "%s: stages must be in [1, 2^24]", fn);
-  REQUIRE(sink != nullptr, "%s: sink is null", fn);
-  if (flops) *flops = ttamd::probe_mfma_loop_flops(stages);
-  return check_hip(ttamd::launch_probe_mfma_loop(stages, (float*)sink, (hipStream_t)stream), fn);
-}
-
 size_t ttamd_gemm_workspace_bytes(int64_t num_rows, int num_experts) {
   if (num_rows < 0 || num_experts < 1) return 0;
   return ttamd::gemm_workspace_bytes(num_rows, num_experts);
@@ -475,11 +467,12 @@ int ttamd_shared_expert_add(const void* x, int64_t num_tokens, int64_t dim, int6
   TRY(check_rows(fn, "out", out, num_tokens, dim));
   if (num_tokens > 0)
     REQUIRE(a_scratch != out && a_scratch != x, "%s: a_scratch must not alias x or out", fn);
+  REQUIRE(std::isnan(swiglu_limit) || swiglu_limit >= 0.f,
+          "%s: swiglu_limit must be NaN (no clamp) or >= 0", fn);
   TRY(check_ws(fn, workspace, workspace_bytes, ttamd::gemm_workspace_bytes(num_tokens, 1)));
   if (num_tokens == 0) return TTAMD_OK;
-  const float lim = (swiglu_limit > 0.f) ? swiglu_limit : NAN;
   return check_hip(ttamd::launch_shared_expert_add(x, (int)num_tokens, (int)dim, (int)hidden, w13_shared,
-                                                   w2_shared, gate_logits, lim, a_scratch, out, workspace,
+                                                   w2_shared, gate_logits, swiglu_limit, a_scratch, out, workspace,
                                                    (hipStream_t)stream),
                    fn);
 }

@@ -163,20 +163,32 @@ __global__ __launch_bounds__(THREADS, 1) void gg_wgrad_dma_kernel(const WgradDma
 #pragma unroll
     for (int j = 0; j < NJ; ++j) f.b[j] = tr8(st + OP_BYTES, brow[j], kk);
   };
-  // Rows >= nvalid of a stage contribute nothing: zero them in the x
-  // fragments.  Lane l holds rows 16 kk + 8 (l >> 5) + {0..3} and + 4 + {0..3}.
+  // Rows >= nvalid of a stage contribute nothing: zero them in both the x
+  // and the dy fragments (the clamped rows loaded there belong to the same
+  // or, for an expert without rows, the previous expert; zeroing only one
+  // operand would turn an Inf or NaN there into NaN instead of the exact
+  // zeros the gradient of an empty expert is).  Lane l holds rows
+  // 16 kk + 8 (l >> 5) + {0..3} and + 4 + {0..3}.
   auto mask_frag = [&](Frag& f, int kk, int nvalid) {
     // element i of the lane's 8 is row 16 kk + 8 (l >> 5) + i: kept if i < rem
     const int rem = nvalid - 16 * kk - 8 * ((l >> 5) & 1);
+    uint32_t keep[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      keep[d] = (2 * d < rem ? 0x0000ffffu : 0u) | (2 * d + 1 < rem ? 0xffff0000u : 0u);
 #pragma unroll
     for (int pb = 0; pb < NPB; ++pb) {
       u32x4_t v = __builtin_bit_cast(u32x4_t, f.a[pb]);
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const uint32_t keep = (2 * d < rem ? 0x0000ffffu : 0u) | (2 * d + 1 < rem ? 0xffff0000u : 0u);
-        v[d] &= keep;
-      }
+      for (int d = 0; d < 4; ++d) v[d] &= keep[d];
       f.a[pb] = __builtin_bit_cast(bf16x8_t, v);
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      u32x4_t v = __builtin_bit_cast(u32x4_t, f.b[j]);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) v[d] &= keep[d];
+      f.b[j] = __builtin_bit_cast(bf16x8_t, v);
     }
   };
 

@@ -43,10 +43,6 @@ size_t gemm_workspace_bytes(int64_t M, int E);
 // The next forward grouped-GEMM launch records these events around its main
 // kernel on its stream, then the probe disarms (nullptr, nullptr: disarm).
 void gemm_probe_arm(hipEvent_t start, hipEvent_t end);
-// MFMA ceiling probe (probe.hip): the GEMM k loop alone on random LDS data,
-// `stages` 64-wide stages per CU; flops of one launch.
-double probe_mfma_loop_flops(int64_t stages);
-hipError_t launch_probe_mfma_loop(int64_t stages, float* sink, hipStream_t stream);
 hipError_t launch_grouped_mm(const void* x, const void* w, const int* offs, int M, int E, int N,
                              int K, void* out, void* ws, hipStream_t stream);
 hipError_t launch_grouped_mm_swiglu(const void* x, const void* w13, const int* offs, int M,

@@ -118,13 +118,17 @@ class CombineFn(torch.autograd.Function):
 class HIPMoeTokenUnpermute(torch.autograd.Function):
     """Functional unpermute with backward; same contract as the reference's
     NPUMoeTokenUnpermute (torchtitanturbo/models/common/npu_permute.py:15-53):
-    probs=None, top_k=1, empty input passes through."""
+    probs=None, top_k=1, empty input passes through.  With one choice per
+    row and no probs the unpermute is a pure row scatter,
+    out[sorted_indices[j]] = permuted_tokens[j], and its backward the
+    matching gather, so both move rows bit for bit in the input's dtype."""
 
     @staticmethod
     def forward(ctx, permuted_tokens, sorted_indices, restore_shape):
         if not permuted_tokens.numel():
             return permuted_tokens
-        out = ops.token_unpermute(permuted_tokens, sorted_indices, None, 1)
+        rows = permuted_tokens.reshape(-1, permuted_tokens.shape[-1])
+        out = ops.scatter_rows_exact(rows, sorted_indices.to(torch.int32))
         ctx.restore_shape = restore_shape
         ctx.save_for_backward(sorted_indices)
         return out.view(restore_shape)
@@ -135,10 +139,33 @@ class HIPMoeTokenUnpermute(torch.autograd.Function):
             return unpermuted_tokens_grad, None, None
         if ctx.needs_input_grad[0]:
             (sorted_indices,) = ctx.saved_tensors
-            g = unpermuted_tokens_grad.reshape(-1, unpermuted_tokens_grad.shape[-1]).to(_BF16).contiguous()
-            act_grad, _ = ops.token_unpermute_grad(g, sorted_indices, None, None, 1)
+            g = unpermuted_tokens_grad.reshape(-1, unpermuted_tokens_grad.shape[-1])
+            act_grad = ops.gather_rows_exact(g, sorted_indices.to(torch.int32))
             return act_grad, None, None
         return None, None, None
+
+
+class TokenPermuteFn(torch.autograd.Function):
+    """permuted[j] = rows[sorted_indices[j]], sorted_indices the stable order of
+    the row labels (torch_npu.npu_moe_token_permute with one label per row,
+    npu_permute.py:74-76).  Rows move bit for bit in their own dtype; the
+    backward scatters the gradient rows back, grad_rows[sorted_indices[j]] =
+    grad_permuted[j] (npu_moe_token_permute's autograd)."""
+
+    @staticmethod
+    def forward(ctx, rows, labels, num_labels):
+        r = ops.route(labels, num_labels)
+        permuted = ops.gather_rows_exact(rows, r.sorted_indices)
+        ctx.save_for_backward(r.sorted_indices)
+        ctx.mark_non_differentiable(r.sorted_indices)
+        return permuted, r.sorted_indices
+
+    @staticmethod
+    def backward(ctx, grad_permuted, _grad_idx):
+        (sorted_indices,) = ctx.saved_tensors
+        if not ctx.needs_input_grad[0]:
+            return None, None, None
+        return ops.scatter_rows_exact(grad_permuted.contiguous(), sorted_indices), None, None
 
 
 def run_experts_grouped_mm(

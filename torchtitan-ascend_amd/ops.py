@@ -262,6 +262,48 @@ def dispatch_rows(
     return out
 
 
+def _rows_as_bf16(name: str, t: torch.Tensor) -> torch.Tensor:
+    """A contiguous 2-D tensor of 2- or 4-byte elements viewed as bf16 bit
+    pairs [rows, cols * elsize / 2]: the row movers copy 16-byte chunks
+    unchanged when no scale is applied, so rows of any such dtype move bit
+    for bit."""
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    if t.element_size() not in (2, 4) or t.dtype.is_complex:
+        raise TypeError(f"{name}: rows of {t.dtype} cannot be moved (2- or 4-byte elements only)")
+    return t.contiguous().view(_BF16)
+
+
+def gather_rows_exact(x: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
+    """out[j] = x[index[j]], bit for bit, for bf16 / fp16 / fp32 rows."""
+    dev = _gpu("x", x)
+    index = _want("index", index, torch.int32)
+    _same_device(dev, index=index)
+    xv = _rows_as_bf16("x", x)
+    rows, W = index.numel(), xv.shape[1]
+    out = torch.empty(rows, W, dtype=_BF16, device=dev)
+    if W % 8:
+        raise ValueError(f"row width of {x.shape[1]} {x.dtype} elements is not a multiple of 16 bytes")
+    _lib.call("ttamd_moe_gather_rows", _p(xv), _p(index), None, xv.shape[0], rows, W, 1, _p(out), _stream(dev))
+    return out.view(x.dtype)
+
+
+def scatter_rows_exact(x: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
+    """out[index[j]] = x[j], bit for bit (index a permutation of the rows)."""
+    dev = _gpu("x", x)
+    index = _want("index", index, torch.int32)
+    _same_device(dev, index=index)
+    xv = _rows_as_bf16("x", x)
+    if index.numel() != xv.shape[0]:
+        raise ValueError(f"index has {index.numel()} entries for {xv.shape[0]} rows")
+    T, W = xv.shape
+    if W % 8:
+        raise ValueError(f"row width of {x.shape[1]} {x.dtype} elements is not a multiple of 16 bytes")
+    out = torch.empty(T, W, dtype=_BF16, device=dev)
+    _lib.call("ttamd_moe_dispatch_rows", _p(xv), _p(index), None, T, W, 1, _p(out), _stream(dev))
+    return out.view(x.dtype)
+
+
 def token_permute(
     tokens: torch.Tensor, indices: torch.Tensor, num_experts: int, return_counts: bool = False
 ):
@@ -427,26 +469,6 @@ def probe_next_gemm(start: "torch.cuda.Event | None", end: "torch.cuda.Event | N
         if not e.cuda_event:
             e.record()
     _lib.call("ttamd_probe_next_gemm", ctypes.c_void_p(start.cuda_event), ctypes.c_void_p(end.cuda_event))
-
-
-def mfma_loop_ceiling(device: torch.device | None = None, stages: int = 4096, reps: int = 10,
-                      warmup: int = 20) -> float:
-    """bf16 MFMA rate (TFLOP/s) of the grouped GEMM's k loop alone on random
-    operands (ttamd_probe_mfma_loop), timed with events on the current
-    stream: the ceiling a bf16 GEMM on realistic data approaches on this GPU."""
-    dev = torch.device(device or "cuda")
-    sink = torch.zeros(1, dtype=torch.float32, device=dev)
-    flops = ctypes.c_double(0.0)
-    st = _stream(dev)
-    for _ in range(warmup):
-        _lib.call("ttamd_probe_mfma_loop", stages, ctypes.byref(flops), _p(sink), st)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        _lib.call("ttamd_probe_mfma_loop", stages, ctypes.byref(flops), _p(sink), st)
-    e1.record()
-    torch.cuda.synchronize(dev)
-    return flops.value * reps / (e0.elapsed_time(e1) * 1e-3) / 1e12
 
 
 def _offs(offs: torch.Tensor, dev: torch.device) -> torch.Tensor:

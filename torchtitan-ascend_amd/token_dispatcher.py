@@ -19,7 +19,7 @@ from dataclasses import dataclass
 import torch
 
 from . import ops
-from .functional import CombineFn, DispatchFn, HIPMoeTokenUnpermute
+from .functional import CombineFn, DispatchFn, HIPMoeTokenUnpermute, TokenPermuteFn
 from .protocol import AllToAllTokenDispatcher, GroupedExperts, ModelConfigConverter
 
 
@@ -84,11 +84,11 @@ class HipTokenDispatcher(AllToAllTokenDispatcher):
         returns (input_shape, permuted_input, permuted_indices, num_tokens_per_expert).
         """
         labels = ops.group_labels(num_tokens_per_expert_group, num_local_experts, routed_input.shape[0])
-        permuted, permuted_indices = ops.token_permute(
-            routed_input.to(torch.bfloat16).contiguous(), labels, num_local_experts
-        )
+        # rows move bit for bit in routed_input's dtype, with autograd (the
+        # backward scatters the gradient rows back)
+        permuted, permuted_indices = TokenPermuteFn.apply(routed_input, labels, num_local_experts)
         num_tokens_per_expert = num_tokens_per_expert_group.view(ep_size, -1).sum(0)
-        return routed_input.shape, permuted.to(routed_input.dtype), permuted_indices, num_tokens_per_expert
+        return routed_input.shape, permuted, permuted_indices, num_tokens_per_expert
 
     def _unpermute(self, routed_output, input_shape, permuted_indices):
         return HIPMoeTokenUnpermute.apply(routed_output, permuted_indices, input_shape)
