@@ -25,7 +25,7 @@ def _counts(kind, M, E, rng):
         cut = np.sort(rng.integers(0, M + 1, E - 1))
         return np.diff(np.concatenate([[0], cut, [M]]))
     if kind == "zipf":
-        return zipf_counts(M, E, 1.2, max(1, E - E // 8), rng)
+        return zipf_counts(M, E, 1.2, max(1, E - max(1, E // 8)), rng)
     raise ValueError(kind)
 
 

@@ -23,7 +23,8 @@ def _counts(kind, M, E, rng):
         cut = np.sort(rng.integers(0, M + 1, E - 1))
         return np.diff(np.concatenate([[0], cut, [M]]))
     if kind == "zipf":
-        return zipf_counts(M, E, 1.2, max(1, E - E // 8), rng)
+        # at least one empty expert whenever E > 1 (E // 8 of them for E >= 16)
+        return zipf_counts(M, E, 1.2, max(1, E - max(1, E // 8)), rng)
     if kind == "one":
         c = np.zeros(E, np.int64)
         c[E // 2] = M

@@ -206,7 +206,7 @@ def test_regroup_permute_autograd(pkg, dtype):
     assert permuted.dtype == dtype and permuted.grad_fn is not None
     _, ref_s, _ = O.regroup_permute(x, counts_group, ep, E_loc)
     np.testing.assert_array_equal(pidx.cpu().numpy(), ref_s)
-    np.testing.assert_array_equal(permuted.detach().cpu().numpy(), x[ref_s])
+    np.testing.assert_array_equal(permuted.detach().float().cpu().numpy(), x[ref_s])
     g = (rng.standard_normal((M, D))).astype(np.float32)
     permuted.backward(torch.from_numpy(g).to(DEV).to(dtype))
     ref_grad = np.empty_like(g)
@@ -217,7 +217,7 @@ def test_regroup_permute_autograd(pkg, dtype):
     y = permuted.detach().requires_grad_(True)
     back = disp._unpermute(y, shape, pidx)
     assert back.dtype == dtype
-    np.testing.assert_array_equal(back.detach().cpu().numpy(), xd.detach().cpu().numpy())
+    np.testing.assert_array_equal(back.detach().float().cpu().numpy(), xd.detach().float().cpu().numpy())
     back.backward(torch.from_numpy(g).to(DEV).to(dtype))
     np.testing.assert_array_equal(y.grad.float().cpu().numpy(),
                                   torch.from_numpy(g).to(dtype).float().numpy()[ref_s])
