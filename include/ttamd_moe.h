@@ -121,6 +121,32 @@ int ttamd_moe_route(const void* labels, int labels_are_int64, int64_t num_flat,
                     size_t workspace_bytes, void* stream);
 
 /*
+ * ttamd_moe_route without a workspace argument: it allocates nothing.
+ * No counterpart in the reference.  It is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops and
+ * harnesses that forbid hipMalloc.
+ *   Same arguments (minus the workspace), outputs and bit-exact results as
+ *   ttamd_moe_route.  The per-chunk histogram lives in a device array the
+ *   library holds on each device it runs on, TTAMD_ROUTE_NOALLOC_WORKSPACE_BYTES
+ *   long, from the first call on that device until the process ends.
+ *   Limit: the histogram, (E + 1) * ceil(num_flat / 1024) int32, must fit
+ *   that array (at most 2^20 ints: e.g. up to 2^20 labels with E <= 1023);
+ *   larger calls are rejected with TTAMD_EINVAL and launch nothing.
+ *   Every call on one device shares that device's array: calls that overlap
+ *   on one device (other streams, other host threads) race and give wrong
+ *   results, so serialise them.  The array keeps the last call's contents;
+ *   nothing in it has to start at zero.  The device is the one `stream`
+ *   belongs to (the current device for a NULL stream).
+ */
+#define TTAMD_ROUTE_NOALLOC_WORKSPACE_BYTES ((size_t)4 << 20)
+int ttamd_moe_route_noalloc(const void* labels, int labels_are_int64,
+                            int64_t num_flat, int num_experts,
+                            const float* scores, int32_t* counts,
+                            int32_t* offsets, int32_t* sorted_indices,
+                            int32_t* inverse, float* sorted_scores,
+                            void* stream);
+
+/*
  * Row gather of the permute: out[j] = in[src_index[j] / topk], optionally
  * multiplied by row_scale[j] in fp32 and rounded to bf16 once (upstream
  * dispatch with score_before_experts).  bf16 [num_in_rows, hidden] ->

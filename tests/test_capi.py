@@ -114,3 +114,19 @@ def test_probes_reject_bad_arguments():
     assert "both events or neither" in msg
     # disarming touches no GPU state
     assert lib.ttamd_probe_next_gemm(None, None) == 0
+
+
+def test_route_noalloc_rejects_oversize_and_bad_arguments():
+    """The allocation-free route refuses, on the host, sizes whose histogram
+    would not fit the library's per-device array, and the usual bad arguments."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    # 2^22 labels over 1024 experts: (1025 * 4096) ints > 2^20
+    msg = _err(lib.ttamd_moe_route_noalloc(p, 1, 1 << 22, 1024, None, p, p, p, p, None, None))
+    assert "workspace" in msg and "ttamd_moe_route" in msg
+    msg = _err(lib.ttamd_moe_route_noalloc(p, 1, 8, 5000, None, None, None, p, None, None, None))
+    assert "num_experts" in msg
+    msg = _err(lib.ttamd_moe_route_noalloc(p, 1, 8, 4, p, None, None, p, None, None, None))
+    assert "sorted_scores" in msg
+    msg = _err(lib.ttamd_moe_route_noalloc(None, 1, 8, 4, None, None, None, p, None, None, None))
+    assert "null" in msg

@@ -40,6 +40,11 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _i32, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
          _c_void_p, _sz, _c_void_p],
     ),
+    "ttamd_moe_route_noalloc": (
+        _i32,
+        [_c_void_p, _i32, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p],
+    ),
     "ttamd_moe_gather_rows": (
         _i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i32, _c_void_p, _c_void_p]
     ),

@@ -153,15 +153,21 @@ size_t ttamd_route_workspace_bytes(int64_t num_flat, int num_experts) {
   return ttamd::route_workspace_bytes(num_flat, num_experts);
 }
 
-static int route_checks(const char* fn, const void* labels, int64_t M, int E, const float* scores,
-                        const int32_t* sorted, const float* sorted_scores, const void* ws,
-                        size_t ws_bytes) {
+static int route_arg_checks(const char* fn, const void* labels, int64_t M, int E, const float* scores,
+                            const int32_t* sorted, const float* sorted_scores) {
   REQUIRE(M >= 0 && M <= (1 << 28), "%s: number of labels out of range (%lld)", fn,
           (long long)M);
   REQUIRE(E >= 1 && E <= 1024, "%s: num_experts must be in [1, 1024] (got %d)", fn, E);
   if (M > 0) REQUIRE(labels && sorted, "%s: null pointer argument", fn);
   REQUIRE((scores == nullptr) == (sorted_scores == nullptr),
           "%s: scores and sorted_scores must be given together", fn);
+  return TTAMD_OK;
+}
+
+static int route_checks(const char* fn, const void* labels, int64_t M, int E, const float* scores,
+                        const int32_t* sorted, const float* sorted_scores, const void* ws,
+                        size_t ws_bytes) {
+  TRY(route_arg_checks(fn, labels, M, E, scores, sorted, sorted_scores));
   TRY(check_ws(fn, ws, ws_bytes, ttamd::route_workspace_bytes(M, E)));
   return TTAMD_OK;
 }
@@ -176,6 +182,25 @@ int ttamd_moe_route(const void* labels, int labels_are_int64, int64_t num_flat, 
   return check_hip(ttamd::launch_route(labels, labels_are_int64 != 0, (int)num_flat, num_experts,
                                        scores, counts, offsets, sorted_indices, inverse,
                                        sorted_scores, workspace, (hipStream_t)stream),
+                   fn);
+}
+
+int ttamd_moe_route_noalloc(const void* labels, int labels_are_int64, int64_t num_flat,
+                            int num_experts, const float* scores, int32_t* counts, int32_t* offsets,
+                            int32_t* sorted_indices, int32_t* inverse, float* sorted_scores,
+                            void* stream) {
+  const char* fn = "ttamd_moe_route_noalloc";
+  TRY(route_arg_checks(fn, labels, num_flat, num_experts, scores, sorted_indices, sorted_scores));
+  const size_t need = ttamd::route_hist_bytes(num_flat, num_experts);
+  REQUIRE(need <= ttamd::route_scratch_bytes(),
+          "%s: %lld labels over %d experts need %zu bytes of route workspace, more than the %zu bytes "
+          "the library holds per device; use ttamd_moe_route with a caller workspace",
+          fn, (long long)num_flat, num_experts, need, ttamd::route_scratch_bytes());
+  void* ws = nullptr;
+  TRY(check_hip(ttamd::route_scratch((hipStream_t)stream, &ws), fn));
+  return check_hip(ttamd::launch_route(labels, labels_are_int64 != 0, (int)num_flat, num_experts,
+                                       scores, counts, offsets, sorted_indices, inverse,
+                                       sorted_scores, ws, (hipStream_t)stream),
                    fn);
 }
 

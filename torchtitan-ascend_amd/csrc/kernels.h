@@ -10,9 +10,16 @@ namespace ttamd {
 
 // routing.hip
 size_t route_workspace_bytes(int64_t M, int E);
+// Bytes of the per-chunk histogram the route kernels read and write.
+size_t route_hist_bytes(int64_t M, int E);
 hipError_t launch_route(const void* labels, bool is64, int M, int E, const float* scores,
                         int* counts, int* offsets, int* sorted_idx, int* inverse,
                         float* sorted_scores, void* ws, hipStream_t stream);
+// The library-owned route workspace of the device that runs `stream` (the
+// current device for a null stream): its size, and its device address
+// (looked up once per device, then cached).
+size_t route_scratch_bytes();
+hipError_t route_scratch(hipStream_t stream, void** ptr);
 hipError_t launch_gather_rows(const void* in, const int* src, const float* scale,
                               bool scale_by_src, int n_in, int n_src_max, int rows, int hidden,
                               int div, void* out, hipStream_t stream);

@@ -18,7 +18,9 @@
 // into the valid range, so a corrupt index array yields wrong values, never
 // an out-of-bounds access.
 #include <algorithm>
+#include <mutex>
 
+#include "../../include/ttamd_moe.h"
 #include "common.h"
 #include "kernels.h"
 
@@ -201,9 +203,56 @@ __global__ __launch_bounds__(kRouteThreads) void route_rank_kernel(
   }
 }
 
-size_t route_workspace_bytes(int64_t M, int E) {
+size_t route_hist_bytes(int64_t M, int E) {
   const int64_t nchunks = (M + kRouteChunk - 1) / kRouteChunk;
-  return (size_t)((E + 1) * nchunks) * sizeof(int) + 256;
+  return (size_t)((E + 1) * nchunks) * sizeof(int);
+}
+
+size_t route_workspace_bytes(int64_t M, int E) { return route_hist_bytes(M, E) + 256; }
+
+// ---------------------------------------------------------------------------
+// Library-owned route workspace (the allocation-free entry point).
+//
+// `scratch` is a file-scope device array: every device the library runs on
+// holds its own copy, at its own address, from the moment the code object is
+// loaded there until the process ends.  Host code never passes `scratch`
+// itself to a kernel (on the host that name is a stand-in, not a device
+// address): the address of each device's copy is looked up once per device
+// with hipGetSymbolAddress, with that device current, and cached here.
+// ---------------------------------------------------------------------------
+constexpr size_t kRouteScratchBytes = TTAMD_ROUTE_NOALLOC_WORKSPACE_BYTES;
+static __device__ __align__(256) int scratch[kRouteScratchBytes / sizeof(int)];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+size_t route_scratch_bytes() { return kRouteScratchBytes; }
+
+hipError_t route_scratch(hipStream_t stream, void** ptr) {
+  *ptr = nullptr;
+  int dev = 0;
+  hipError_t err = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  if (dev < 0 || dev >= kMaxScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int prev = 0;
+    err = hipGetDevice(&prev);
+    if (err != hipSuccess) return err;
+    if (prev != dev && (err = hipSetDevice(dev)) != hipSuccess) return err;
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (prev != dev) {
+      const hipError_t back = hipSetDevice(prev);
+      if (err == hipSuccess) err = back;
+    }
+    if (err != hipSuccess) return err;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return hipSuccess;
 }
 
 hipError_t launch_route(const void* labels, bool is64, int M, int E,
