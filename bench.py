@@ -3,9 +3,11 @@
 Default workload (Qwen3-30B-A3B shape, MoE layer
 forward, bf16): T=8192 tokens, D=2048, H=768, E=128 experts, top-8 softmax
 router with renormalised weights.  One step = router (gate GEMM split over D
-+ fp32 softmax + top-k + renorm) -> route (histogram + stable sort) ->
++ fp32 softmax + top-k + renorm + histogram) -> stable sort + tile table ->
 grouped GEMM w13 + SwiGLU with the permute gather in its loads -> grouped
-GEMM w2 + score + un-permute -> K-way sum, on inputs already resident in HBM.
+GEMM w2 + score + un-permute -> K-way sum, on inputs already resident in HBM:
+two C-ABI calls (ttamd_router_route, ttamd_moe_experts_forward), six kernel
+launches.  The per-stage breakdown runs the same kernels one op at a time.
 
 Prints ONE JSON line (bench contract) with `roofline` for the dominant
 kernel (the w13 grouped GEMM, timed in every timed step by an event pair the
@@ -56,6 +58,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--staged", action="store_true",
+                    help="time the op-at-a-time path (router, route, then each GEMM and the sum as its own call) "
+                         "instead of the two fused C-ABI calls")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device copy (reference for the PMC byte counters) and exit")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -143,11 +148,25 @@ def main():
         sw2 = (torch.randn(D, H, device=dev) * 0.02).to(torch.bfloat16)
 
     def step_forward(ev=None):
+        if ev is None and not fp8 and not args.staged:
+            # The timed step: two C-ABI calls.  ttamd_router_route (gate GEMM
+            # + score + top-k + histogram, then the stable order and the
+            # GEMMs' tile table) and ttamd_moe_experts_forward (w13 + SwiGLU
+            # with the permute gather in its loads, w2 + score + un-permute,
+            # K-way sum, both GEMMs on that tile table).
+            if zipf_idx is not None:
+                r = ops.route(zipf_idx, E, zipf_scores)
+            else:
+                _, _, r = ops.router_route(x, w_router, K, cfg["router"], cfg["norm"], with_inverse=False)
+            out = ops.experts_forward(x, r, w13, w2, K, cfg["score_before"])
+            return F.shared_expert_combine(out, x, sw13, sw2) if shared else out
+        # stage breakdown: the same kernels one op at a time, events around each
         scores, idx = timed_router(ev)
         if fp8:
             return F.moe_experts_forward_fp8(x, scores, idx, w13q, s13, w2q, s2, E, cfg["score_before"],
                                              stage_events=ev)
-        out = F.moe_experts_forward(x, scores, idx, w13, w2, E, cfg["score_before"], stage_events=ev)
+        out = F.moe_experts_forward(x, scores, idx, w13, w2, E, cfg["score_before"],
+                                    stage_events=ev if ev is not None else {})
         if shared:
             # no autograd here: one fused pass, the shared w2 GEMM adds into out
             pair = ev.setdefault("shared_expert", (torch.cuda.Event(enable_timing=True),

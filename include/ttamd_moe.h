@@ -95,6 +95,40 @@ int ttamd_router_fused(const void* x, const void* w_router,
                        void* logits_out, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/*
+ * Router + dispatch order in one call: the router of ttamd_router_fused,
+ * then the histogram and stable order of ttamd_moe_route over its picks
+ * (selected_experts_indices.view(-1)), with no round trip between them.
+ * Replaces upstream TokenChoiceTopKRouter.forward (closed form
+ * torchtitanturbo/models/qwen3_5/model.py:752-766) followed by dispatch's
+ * histc + stable argsort (reached from npu_gmm.py:106-108).
+ *   Outputs: top_scores / top_indices as ttamd_router_fused; counts,
+ *   offsets, sorted_indices, inverse, sorted_scores as ttamd_moe_route
+ *   (counts, offsets, inverse, sorted_scores nullable; sorted_scores[j] =
+ *   top_scores.view(-1)[sorted_indices[j]]).
+ *   tokens_per_expert (nullable, fp32 [E]) += counts: upstream's
+ *   load-balancing accumulator (router.tokens_per_expert.add_(histc)).
+ *   gemm_plan (nullable, ttamd_gemm_workspace_bytes(T*topk, E) bytes)
+ *   receives the token-tile table of the expert-sorted rows that
+ *   ttamd_moe_experts_forward can use for both grouped GEMMs.
+ * Same argument limits as ttamd_router_fused; workspace:
+ * ttamd_router_route_workspace_bytes.  Launches: gate GEMM, score + top-k
+ * + histogram, rank (the histogram scan folded in for (E + 1) *
+ * ceil(T*topk / 1024) <= 32768).
+ */
+size_t ttamd_router_route_workspace_bytes(int64_t num_tokens, int num_experts,
+                                          int64_t dim, int topk);
+int ttamd_router_route(const void* x, const void* w_router,
+                       const float* expert_bias, int64_t num_tokens,
+                       int num_experts, int64_t dim, int topk, int score_func,
+                       int renorm, float renorm_eps, float route_scale,
+                       float* top_scores, int64_t* top_indices,
+                       int32_t* counts, int32_t* offsets,
+                       int32_t* sorted_indices, int32_t* inverse,
+                       float* sorted_scores, float* tokens_per_expert,
+                       void* gemm_plan, size_t gemm_plan_bytes,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* Bytes of device workspace ttamd_moe_route / ttamd_moe_token_permute need. */
 size_t ttamd_route_workspace_bytes(int64_t num_flat, int num_experts);
 
@@ -322,6 +356,41 @@ int ttamd_grouped_mm_unpermute(const void* a, const void* w2,
                                int64_t num_dest_rows, void* out,
                                void* workspace, size_t workspace_bytes,
                                void* stream);
+
+/*
+ * The expert stage of the MoE layer forward (inference) in one call:
+ * NpuGroupedExperts.forward's dispatch -> _run_experts_grouped_mm ->
+ * combine (torchtitanturbo/models/common/npu_gmm.py:100-110 with :21-40),
+ * given the routing of ttamd_moe_route / ttamd_router_route:
+ *   routed[j] = tokens[sorted_indices[j] / topk] (* sorted_scores[j] when
+ *               score_before_experts, rounded to bf16 once);
+ *   a = silu(gate) * up of routed @ w13[e]^T (clamp as
+ *       ttamd_grouped_mm_swiglu);
+ *   y[j] = a[j] @ w2[e]^T (* sorted_scores[j] when the score comes after);
+ *   out[t] = sum_k y[j(t, k)]  (fp32 sum, bf16 out; topk = 1: a scatter).
+ * tokens bf16 [T, D]; offs inclusive int32 [E] (ttamd_moe_route's offsets
+ * + 1); w13 [E, 2H, D], w2 [E, D, H]; out bf16 [T, D].  Every label must be
+ * in [0, E) (offs[E-1] = T * topk).  D % 128 == 0, H % 64 == 0.
+ * Without score_before_experts the gather is fused into the w13 GEMM's
+ * loads (the routed copy is never written).  gemm_plan (nullable): the tile
+ * table from ttamd_router_route for these offs; both GEMMs use it (null:
+ * one is built in the workspace).  workspace:
+ * ttamd_moe_experts_forward_workspace_bytes (tile table, a, and for
+ * score-before the routed rows, for topk > 1 y).
+ */
+size_t ttamd_moe_experts_forward_workspace_bytes(int64_t num_tokens,
+                                                 int64_t dim, int64_t hidden,
+                                                 int num_experts, int topk,
+                                                 int score_before_experts);
+int ttamd_moe_experts_forward(const void* tokens, int64_t num_tokens,
+                              int64_t dim, int64_t hidden, int num_experts,
+                              int topk, const int32_t* sorted_indices,
+                              const int32_t* offs, const float* sorted_scores,
+                              int score_before_experts, float swiglu_limit,
+                              const void* w13, const void* w2, void* out,
+                              const void* gemm_plan, size_t gemm_plan_bytes,
+                              void* workspace, size_t workspace_bytes,
+                              void* stream);
 
 /* out[t] = sum_{k<topk} in[t*topk + k] (fp32 accumulate, bf16 out). */
 int ttamd_moe_sum_topk(const void* in, int64_t num_tokens, int64_t hidden,

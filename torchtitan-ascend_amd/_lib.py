@@ -34,6 +34,13 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i64, _i32, _i32, _i32, _f32, _f32, _c_void_p, _c_void_p,
          _c_void_p, _c_void_p, _sz, _c_void_p],
     ),
+    "ttamd_router_route_workspace_bytes": (_sz, [_i64, _i32, _i64, _i32]),
+    "ttamd_router_route": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i64, _i32, _i32, _i32, _f32, _f32, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _sz, _c_void_p, _sz,
+         _c_void_p],
+    ),
     "ttamd_route_workspace_bytes": (_sz, [_i64, _i32]),
     "ttamd_moe_route": (
         _i32,
@@ -85,6 +92,12 @@ SIGNATURES: dict[str, tuple] = {
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i64, _i64, _c_void_p, _c_void_p, _i64, _c_void_p,
          _c_void_p, _sz, _c_void_p],
+    ),
+    "ttamd_moe_experts_forward_workspace_bytes": (_sz, [_i64, _i64, _i64, _i32, _i32, _i32]),
+    "ttamd_moe_experts_forward": (
+        _i32,
+        [_c_void_p, _i64, _i64, _i64, _i32, _i32, _c_void_p, _c_void_p, _c_void_p, _i32, _f32, _c_void_p,
+         _c_void_p, _c_void_p, _c_void_p, _sz, _c_void_p, _sz, _c_void_p],
     ),
     "ttamd_moe_sum_topk": (_i32, [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p]),
     "ttamd_shared_expert_add": (

@@ -204,6 +204,103 @@ int ttamd_moe_route_noalloc(const void* labels, int labels_are_int64, int64_t nu
                    fn);
 }
 
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+size_t ttamd_router_route_workspace_bytes(int64_t num_tokens, int num_experts, int64_t dim, int topk) {
+  if (num_tokens < 0 || num_experts < 1 || dim < 64 || topk < 1) return 0;
+  return align256(ttamd::router_workspace_bytes(num_tokens, num_experts, dim)) +
+         ttamd::route_workspace_bytes(num_tokens * topk, num_experts);
+}
+
+int ttamd_router_route(const void* x, const void* w_router, const float* expert_bias, int64_t num_tokens,
+                       int num_experts, int64_t dim, int topk, int score_func, int renorm, float renorm_eps,
+                       float route_scale, float* top_scores, int64_t* top_indices, int32_t* counts,
+                       int32_t* offsets, int32_t* sorted_indices, int32_t* inverse, float* sorted_scores,
+                       float* tokens_per_expert, void* gemm_plan, size_t gemm_plan_bytes, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  const char* fn = "ttamd_router_route";
+  REQUIRE(num_tokens >= 0 && num_tokens <= (1 << 24), "%s: num_tokens out of range", fn);
+  REQUIRE(num_experts >= 1 && num_experts <= 256, "%s: num_experts must be in [1, 256]", fn);
+  REQUIRE(topk >= 1 && topk <= 16 && topk <= num_experts, "%s: topk must be in [1, min(16, E)]", fn);
+  REQUIRE(score_func == TTAMD_SCORE_SOFTMAX || score_func == TTAMD_SCORE_SIGMOID,
+          "%s: unknown score_func %d", fn, score_func);
+  REQUIRE(dim >= 64 && dim % 64 == 0 && dim <= (1 << 20), "%s: dim must be a positive multiple of 64", fn);
+  REQUIRE((int64_t)num_experts * dim * 2 < kI32Max && 128 * dim * 2 < kI32Max, "%s: router weight too large",
+          fn);
+  const int64_t M = num_tokens * topk;
+  REQUIRE(M <= (1 << 28), "%s: too many routed rows", fn);
+  REQUIRE(num_tokens == 0 || (x && w_router && top_scores && top_indices && sorted_indices),
+          "%s: null pointer argument", fn);
+  REQUIRE(w_router != nullptr, "%s: w_router is null", fn);
+  REQUIRE(aligned16(x) && aligned16(w_router), "%s: x and w_router must be 16-byte aligned", fn);
+  const size_t rbytes = align256(ttamd::router_workspace_bytes(num_tokens, num_experts, dim));
+  TRY(check_ws(fn, workspace, workspace_bytes, ttamd_router_route_workspace_bytes(num_tokens, num_experts, dim, topk)));
+  if (gemm_plan) {
+    REQUIRE(aligned16(gemm_plan), "%s: gemm_plan must be 16-byte aligned", fn);
+    REQUIRE(gemm_plan_bytes >= ttamd::gemm_workspace_bytes(M, num_experts),
+            "%s: gemm_plan too small (%zu bytes, need %zu)", fn, gemm_plan_bytes,
+            ttamd::gemm_workspace_bytes(M, num_experts));
+  }
+  hipStream_t s = (hipStream_t)stream;
+  int* hist = (int*)((char*)workspace + rbytes);
+  TRY(check_hip(ttamd::launch_router_hist(x, w_router, expert_bias, (int)num_tokens, num_experts, (int)dim, topk,
+                                          score_func, renorm, renorm_eps, route_scale, top_scores, top_indices,
+                                          nullptr, workspace, hist, s),
+                fn));
+  return check_hip(ttamd::launch_route_from_hist(top_indices, true, (int)M, num_experts, top_scores, counts, offsets,
+                                                 sorted_indices, inverse, sorted_scores, hist, tokens_per_expert,
+                                                 gemm_plan, ttamd::gemm_fwd_tile_rows(), s),
+                   fn);
+}
+
+size_t ttamd_moe_experts_forward_workspace_bytes(int64_t num_tokens, int64_t dim, int64_t hidden,
+                                                 int num_experts, int topk, int score_before_experts) {
+  if (num_tokens < 0 || dim < 1 || hidden < 1 || num_experts < 1 || topk < 1) return 0;
+  return ttamd::moe_experts_forward_workspace_bytes(num_tokens, dim, hidden, num_experts, topk,
+                                                    score_before_experts != 0 || dim < 128);
+}
+
+int ttamd_moe_experts_forward(const void* tokens, int64_t num_tokens, int64_t dim, int64_t hidden,
+                              int num_experts, int topk, const int32_t* sorted_indices, const int32_t* offs,
+                              const float* sorted_scores, int score_before_experts, float swiglu_limit,
+                              const void* w13, const void* w2, void* out, const void* gemm_plan,
+                              size_t gemm_plan_bytes, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "ttamd_moe_experts_forward";
+  REQUIRE(topk >= 1 && topk <= 64, "%s: topk must be in [1, 64]", fn);
+  REQUIRE(num_tokens >= 0 && num_tokens * topk <= (1 << 28), "%s: num_tokens out of range", fn);
+  const int64_t M = num_tokens * topk;
+  TRY(check_gemm_common(fn, offs, M, num_experts));
+  TRY(check_dim(fn, "dim", dim, 128));
+  TRY(check_dim(fn, "hidden", hidden, 64));
+  REQUIRE(std::isnan(swiglu_limit) || swiglu_limit >= 0.f, "%s: swiglu_limit must be NaN (no clamp) or >= 0",
+          fn);
+  REQUIRE(w13 && aligned16(w13) && w2 && aligned16(w2), "%s: w13 and w2 must be non-null and 16-byte aligned",
+          fn);
+  REQUIRE(num_tokens * dim * 2 <= (int64_t)0xffffffffLL, "%s: tokens must stay below 4 GiB", fn);
+  TRY(check_rows(fn, "tokens", tokens, num_tokens, dim));
+  TRY(check_rows(fn, "out", out, num_tokens, dim));
+  REQUIRE(M * (dim / 8) <= (int64_t(1) << 30) && M * (hidden / 8) <= (int64_t(1) << 30),
+          "%s: too many routed elements (%lld rows)", fn, (long long)M);
+  if (M > 0) REQUIRE(sorted_indices != nullptr, "%s: sorted_indices is null", fn);
+  REQUIRE(score_before_experts == 0 || sorted_scores != nullptr || M == 0,
+          "%s: score_before_experts needs sorted_scores", fn);
+  if (gemm_plan) {
+    REQUIRE(aligned16(gemm_plan), "%s: gemm_plan must be 16-byte aligned", fn);
+    REQUIRE(gemm_plan_bytes >= ttamd::gemm_workspace_bytes(M, num_experts),
+            "%s: gemm_plan too small (%zu bytes, need %zu)", fn, gemm_plan_bytes,
+            ttamd::gemm_workspace_bytes(M, num_experts));
+  }
+  TRY(check_ws(fn, workspace, workspace_bytes,
+               ttamd_moe_experts_forward_workspace_bytes(num_tokens, dim, hidden, num_experts, topk,
+                                                         score_before_experts)));
+  if (M == 0) return TTAMD_OK;
+  return check_hip(ttamd::launch_moe_experts_forward(tokens, (int)num_tokens, (int)dim, (int)hidden, num_experts,
+                                                     topk, sorted_indices, offs, sorted_scores,
+                                                     score_before_experts != 0, swiglu_limit, w13, w2, out,
+                                                     gemm_plan, workspace, (hipStream_t)stream),
+                   fn);
+}
+
 int ttamd_moe_gather_rows(const void* in, const int32_t* src_index, const float* row_scale,
                           int64_t num_in_rows, int64_t num_out_rows, int64_t hidden, int topk,
                           void* out, void* stream) {

@@ -17,50 +17,23 @@ namespace ttamd {
 
 // ---------------------------------------------------------------------------
 // Tile table: token tile i -> {expert, first row, end row}.  Built on the
-// device from the inclusive group offsets, so no count reaches the host.
-// An expert's rows are split into the fewest tiles of at most max_rows rows,
-// of equal height rounded up to 32 rows (540 rows at max_rows = 320 give
-// 2 tiles of 288 rather than 320 + 220).  A null offs means one expert
-// (E == 1) with all M rows.
+// device from the inclusive group offsets, so no count reaches the host
+// (block_tile_table: equal-height tiles of at most max_rows rows per
+// expert).  A null offs means one expert (E == 1) with all M rows.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void tile_map_kernel(const int* __restrict__ offs, int E,
                                                         int M, int max_tiles, int max_rows,
                                                         int4* __restrict__ table,
                                                         int* __restrict__ count) {
-  __shared__ int wave_sums[16];
-  const int tid = threadIdx.x;
-  int r0 = 0, r1 = 0, nt = 0, h = max_rows;
-  if (tid < E) {
+  __shared__ int sh[1024 / kWave + 1];
+  auto range = [&](int e, int& r0, int& r1) {
     // offs == nullptr: one expert owning all M rows
-    const int a = (tid == 0 || !offs) ? 0 : offs[tid - 1];
-    const int b = offs ? offs[tid] : M;
+    const int a = (e == 0 || !offs) ? 0 : offs[e - 1];
+    const int b = offs ? offs[e] : M;
     r0 = min(max(a, 0), M);
     r1 = min(max(b, r0), M);
-    const int c = r1 - r0;
-    if (c > 0) {
-      const int n0 = (c + max_rows - 1) / max_rows;
-      h = (((c + n0 - 1) / n0) + 31) & ~31;
-      nt = (c + h - 1) / h;
-    }
-  }
-  const int incl = wave_inclusive_scan(nt);
-  const int w = tid / kWave, l = lane_id();
-  if (l == kWave - 1) wave_sums[w] = incl;
-  __syncthreads();
-  if (w == 0) {
-    const int v = (l < 16) ? wave_sums[l] : 0;
-    const int vi = wave_inclusive_scan(v);
-    if (l < 16) wave_sums[l] = vi;  // inclusive
-  }
-  __syncthreads();
-  const int start = ((w > 0) ? wave_sums[w - 1] : 0) + incl - nt;
-  const int total = wave_sums[15];
-  for (int t = 0; t < nt; ++t) {
-    const int i = start + t;
-    if (i < max_tiles) table[i] = make_int4(tid, r0 + t * h, min(r0 + (t + 1) * h, r1), 0);
-  }
-  for (int i = total + tid; i < max_tiles; i += 1024) table[i] = make_int4(-1, 0, 0, 0);
-  if (tid == 0) *count = min(total, max_tiles);
+  };
+  block_tile_table<1024>(range, E, max_tiles, max_rows, table, count, sh);
 }
 
 hipError_t launch_tile_map(const int* offs, int E, int M, int max_rows, void* ws, hipStream_t stream) {
@@ -74,6 +47,8 @@ hipError_t launch_tile_map(const int* offs, int E, int M, int max_rows, void* ws
 // Launchers.
 // ---------------------------------------------------------------------------
 int gemm_max_qtiles(int M, int E) { return max_row_tiles(M, E); }
+
+int gemm_fwd_tile_rows() { return kFwdTileRows; }
 
 size_t gemm_workspace_bytes(int64_t M, int E) {
   return (size_t)(max_row_tiles((int)M, E) + 1) * sizeof(int4) + 256;
@@ -102,10 +77,14 @@ static hipError_t probed(hipStream_t stream, F&& main) {
   return hipEventRecord(e1, stream);
 }
 
+// table_ready: `ws` already holds the tile table of these rows (a plan
+// built for kFwdTileRows-row tiles), so no tile-map launch.
 static hipError_t fwd(int epi, FwdGemm g, const int* offs, int E, int M, void* ws,
-                      hipStream_t stream) {
-  hipError_t err = launch_tile_map(offs, E, M, kFwdTileRows, ws, stream);
-  if (err != hipSuccess) return err;
+                      hipStream_t stream, bool table_ready = false) {
+  if (!table_ready) {
+    hipError_t err = launch_tile_map(offs, E, M, kFwdTileRows, ws, stream);
+    if (err != hipSuccess) return err;
+  }
   const TileTable tt = tile_table_in(ws);
   g.table = tt.table;
   g.n_qtiles = tt.count;
@@ -145,6 +124,66 @@ hipError_t launch_grouped_mm_unpermute(const void* act, const void* w2, const in
   g.act = act; g.w = w2; g.kred = H; g.n = D; g.out = out;
   g.row_scale = row_scale; g.dest = dest; g.n_dest = n_dest;
   return fwd(EPI_SCATTER, g, offs, E, M, ws, stream);
+}
+
+// ---- the expert stage of the MoE layer forward in one call ---------------------
+size_t moe_experts_forward_workspace_bytes(int64_t T, int64_t D, int64_t H, int E, int K, bool permute_first) {
+  const int64_t M = T * K;
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  size_t n = al(gemm_workspace_bytes(M, E));                 // tile plan
+  n += al((size_t)M * H * 2);                                // a = swiglu(x w13^T)
+  if (permute_first) n += al((size_t)M * D * 2);             // routed rows
+  if (K > 1) n += al((size_t)M * D * 2);                     // y in flat-slot order
+  return n;
+}
+
+hipError_t launch_moe_experts_forward(const void* tokens, int T, int D, int H, int E, int K,
+                                      const int* sorted_idx, const int* offs, const float* sorted_scores,
+                                      bool score_before, float limit, const void* w13, const void* w2,
+                                      void* out, const void* plan, void* ws, hipStream_t stream) {
+  const int M = T * K;
+  const bool permute_first = score_before || D < 128;
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  char* p = (char*)ws;
+  void* own_plan = p;
+  p += al(gemm_workspace_bytes(M, E));
+  void* a = p;
+  p += al((size_t)M * H * 2);
+  void* routed = nullptr;
+  if (permute_first) {
+    routed = p;
+    p += al((size_t)M * D * 2);
+  }
+  void* y = (K > 1) ? (void*)p : out;
+  hipError_t err;
+  // one tile table for both GEMMs
+  void* tp = const_cast<void*>(plan);
+  if (tp == nullptr) {
+    tp = own_plan;
+    if ((err = launch_tile_map(offs, E, M, kFwdTileRows, tp, stream)) != hipSuccess) return err;
+  }
+  if (permute_first) {
+    err = launch_gather_rows(tokens, sorted_idx, score_before ? sorted_scores : nullptr, false, T, M, M, D, K,
+                             routed, stream);
+    if (err != hipSuccess) return err;
+    FwdGemm g = {};
+    g.act = routed; g.w = w13; g.kred = D; g.n = H; g.out = a; g.limit = limit;
+    err = fwd(EPI_SWIGLU, g, offs, E, M, tp, stream, true);
+  } else {
+    FwdGemm g = {};
+    g.act = tokens; g.act_index = sorted_idx; g.act_div = K; g.n_act = T;
+    g.w = w13; g.kred = D; g.n = H; g.out = a; g.limit = limit;
+    err = fwd(EPI_SWIGLU, g, offs, E, M, tp, stream, true);
+  }
+  if (err != hipSuccess) return err;
+  FwdGemm g2 = {};
+  g2.act = a; g2.w = w2; g2.kred = H; g2.n = D; g2.out = y;
+  g2.row_scale = score_before ? nullptr : sorted_scores;
+  g2.dest = sorted_idx;
+  g2.n_dest = (K > 1) ? M : T;
+  if ((err = fwd(EPI_SCATTER, g2, offs, E, M, tp, stream, true)) != hipSuccess) return err;
+  if (K > 1) return launch_combine(y, nullptr, nullptr, T, K, D, out, stream);
+  return hipSuccess;
 }
 
 // ---- fp8 forward (gemm_fp8.hip) ----------------------------------------------

@@ -42,6 +42,53 @@ inline TileTable tile_table_in(void* ws) {
   return t;
 }
 
+// Builds the tile table with one workgroup of NT threads (every thread
+// calls it; it synchronises the workgroup).  `range(e, r0, r1)` gives the
+// rows [r0, r1) of expert e.  An expert's rows are split into the fewest
+// tiles of at most max_rows rows, of equal height rounded up to 32 rows
+// (540 rows at max_rows = 320 give 2 tiles of 288 rather than 320 + 220);
+// tiles are numbered in expert order.  Entries past the last tile, up to
+// max_tiles, are {-1, 0, 0, 0}.  sh: NT / 64 + 1 ints of LDS.
+template <int NT, typename Range>
+__device__ void block_tile_table(Range range, int E, int max_tiles, int max_rows, int4* __restrict__ table,
+                                 int* __restrict__ count, int* sh) {
+  constexpr int NW = NT / kWave;
+  const int tid = threadIdx.x;
+  const int w = tid / kWave, l = lane_id();
+  int carry = 0;
+  for (int e0 = 0; e0 < E; e0 += NT) {
+    const int e = e0 + tid;
+    int r0 = 0, r1 = 0, nt = 0, h = max_rows;
+    if (e < E) {
+      range(e, r0, r1);
+      const int c = r1 - r0;
+      if (c > 0) {
+        const int n0 = (c + max_rows - 1) / max_rows;
+        h = (((c + n0 - 1) / n0) + 31) & ~31;
+        nt = (c + h - 1) / h;
+      }
+    }
+    const int incl = wave_inclusive_scan(nt);
+    if (l == kWave - 1) sh[w] = incl;
+    __syncthreads();
+    if (w == 0) {
+      const int v = (l < NW) ? sh[l] : 0;
+      const int vi = wave_inclusive_scan(v);
+      if (l < NW) sh[l] = vi;  // inclusive over waves
+    }
+    __syncthreads();
+    const int start = carry + ((w > 0) ? sh[w - 1] : 0) + incl - nt;
+    for (int t = 0; t < nt; ++t) {
+      const int i = start + t;
+      if (i < max_tiles) table[i] = make_int4(e, r0 + t * h, min(r0 + (t + 1) * h, r1), 0);
+    }
+    carry += sh[NW - 1];
+    __syncthreads();  // sh is rewritten by the next round
+  }
+  for (int i = carry + tid; i < max_tiles; i += NT) table[i] = make_int4(-1, 0, 0, 0);
+  if (tid == 0) *count = min(carry, max_tiles);
+}
+
 // Forward GEMM description (gemm_fwd.hip).
 //   act [M][kred] bf16, w [E][N or 2N][kred] bf16.
 //   EPI_SWIGLU: n = H (w holds 2H rows: gate then up), out [M][H], h_out [M][2H].

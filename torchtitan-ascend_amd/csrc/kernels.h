@@ -12,6 +12,21 @@ namespace ttamd {
 size_t route_workspace_bytes(int64_t M, int E);
 // Bytes of the per-chunk histogram the route kernels read and write.
 size_t route_hist_bytes(int64_t M, int E);
+// Histogram geometry: chunks of route_chunk_labels() flat labels, the
+// histogram stored bucket-major, hist[b * num_chunks + chunk].
+int route_num_chunks(int64_t M);
+int route_chunk_labels();
+// The rank pass folds the histogram scan in (one launch) for histograms of
+// at most 32768 entries.
+bool route_fused_scan(int64_t M, int E);
+// Scan + rank from an accumulated histogram: counts, offsets, the stable
+// order; optionally adds the counts to tokens_per_expert and builds the
+// forward GEMMs' tile table (tiles of at most plan_max_rows rows) in `plan`
+// (gemm workspace layout).
+hipError_t launch_route_from_hist(const void* labels, bool is64, int M, int E, const float* scores,
+                                  int* counts, int* offsets, int* sorted_idx, int* inverse,
+                                  float* sorted_scores, int* hist, float* tokens_per_expert,
+                                  void* plan, int plan_max_rows, hipStream_t stream);
 hipError_t launch_route(const void* labels, bool is64, int M, int E, const float* scores,
                         int* counts, int* offsets, int* sorted_idx, int* inverse,
                         float* sorted_scores, void* ws, hipStream_t stream);
@@ -43,10 +58,19 @@ hipError_t launch_router_fused(const void* x, const void* w, const float* bias, 
                                int score_func, int renorm, float renorm_eps, float route_scale,
                                float* top_scores, int64_t* top_idx, void* logits, void* ws,
                                hipStream_t stream);
+// The same router, also accumulating the route histogram of the picks into
+// `hist` ((E + 1) * route_num_chunks(T * K) ints, cleared by the gate GEMM
+// kernel first), ready for launch_route_from_hist.
+hipError_t launch_router_hist(const void* x, const void* w, const float* bias, int T, int E, int D, int K,
+                              int score_func, int renorm, float renorm_eps, float route_scale,
+                              float* top_scores, int64_t* top_idx, void* logits, void* ws, int* hist,
+                              hipStream_t stream);
 
 // gemm.hip
 int gemm_max_qtiles(int M, int E);
 size_t gemm_workspace_bytes(int64_t M, int E);
+// Largest token tile of the bf16 forward / dgrad GEMMs (tile plans are built for it).
+int gemm_fwd_tile_rows();
 // The next forward grouped-GEMM launch records these events around its main
 // kernel on its stream, then the probe disarms (nullptr, nullptr: disarm).
 void gemm_probe_arm(hipEvent_t start, hipEvent_t end);
@@ -66,6 +90,14 @@ hipError_t launch_grouped_mm_unpermute(const void* act, const void* w2, const in
 hipError_t launch_shared_expert_add(const void* x, int T, int D, int H, const void* w13s, const void* w2s,
                                    const float* gate_logits, float limit, void* a_scratch, void* out,
                                    void* ws, hipStream_t stream);
+// The expert stage of the inference forward: (gather [+ score] ->) w13 +
+// SwiGLU -> w2 + score + scatter (-> K-way sum), both GEMMs on one tile
+// table (`plan`, or one built into the workspace when plan is null).
+size_t moe_experts_forward_workspace_bytes(int64_t T, int64_t D, int64_t H, int E, int K, bool permute_first);
+hipError_t launch_moe_experts_forward(const void* tokens, int T, int D, int H, int E, int K,
+                                      const int* sorted_idx, const int* offs, const float* sorted_scores,
+                                      bool score_before, float limit, const void* w13, const void* w2,
+                                      void* out, const void* plan, void* ws, hipStream_t stream);
 hipError_t launch_grouped_mm_dgrad(const void* dy, const void* w, const int* offs, int M, int E,
                                    int N, int K, void* dx, void* ws, hipStream_t stream);
 hipError_t launch_grouped_mm_dgrad_swiglu(const void* dy, const void* w2, const void* h,

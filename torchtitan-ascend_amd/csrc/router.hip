@@ -56,6 +56,8 @@ struct RouterGemmArgs {
   int T, E, D;
   int kstages;      // 64-wide k stages per split
   float* part;      // [S][T][E] fp32
+  int* zero;        // nullable: ints cleared for the top-k kernel's histogram
+  int nzero;
 };
 
 template <int EB>
@@ -77,6 +79,11 @@ __global__ __launch_bounds__(RTHREADS) void router_gemm_kernel(const RouterGemmA
   const int nst = min(a.kstages, a.D / RTK - k0);      // stages of this slice
   const uint32_t lds0 = lds_addr(smem);
   const int64_t ld2 = (int64_t)a.D * 2;
+  if (a.zero) {  // the route histogram the top-k kernel accumulates into
+    const int nb = gridDim.x * gridDim.y;
+    for (int i = (blockIdx.y * gridDim.x + blockIdx.x) * RTHREADS + threadIdx.x; i < a.nzero; i += nb * RTHREADS)
+      a.zero[i] = 0;
+  }
 
   // Instruction i of wave w moves row block rb = 4 i + w (rows 8 rb ..
   // 8 rb + 7): instructions 0..TPW-1 carry token rows, the rest expert rows.
@@ -159,6 +166,10 @@ struct RouterTopkArgs {
   float* scores;      // [T, K]
   int64_t* idx;       // [T, K]
   bf16_t* logits;     // [T, E] or null
+  // nullable: per-chunk expert histogram of the picks (route layout,
+  // hist[e * nchunks + (t * K + k) / chunk]), accumulated with atomics
+  int* hist;
+  int nchunks, chunk;
 };
 
 // (selection value desc, expert id asc) winner, with its unbiased score.
@@ -284,6 +295,24 @@ __global__ __launch_bounds__(256) void router_topk_partials_kernel(const RouterT
     a.scores[(int64_t)t * a.K + gi] = v * a.route_scale;
     a.idx[(int64_t)t * a.K + gi] = my_i;
   }
+  if (a.hist) {
+    // The workgroup's 16 K flat slots (K <= 16) span at most two chunks:
+    // count them in LDS, then one atomic per nonzero (expert, chunk).
+    __shared__ int lh[2 * kRouterMaxE];
+    const int c0 = (int)(((int64_t)blockIdx.x * 16 * a.K) / a.chunk);
+    for (int i = threadIdx.x; i < 2 * a.E; i += 256) lh[i] = 0;
+    __syncthreads();
+    if (gi < a.K && valid) {
+      const int c = (int)(((int64_t)t * a.K + gi) / a.chunk) - c0;  // 0 or 1
+      atomicAdd(&lh[min(max(c, 0), 1) * a.E + my_i], 1);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 2 * a.E; i += 256) {
+      const int n = lh[i];
+      const int c = c0 + i / a.E;
+      if (n > 0 && c < a.nchunks) atomicAdd(&a.hist[(int64_t)(i % a.E) * a.nchunks + c], n);
+    }
+  }
 }
 
 template <int EB>
@@ -325,6 +354,14 @@ hipError_t launch_router_fused(const void* x, const void* w, const float* bias, 
                                int score_func, int renorm, float renorm_eps, float route_scale,
                                float* top_scores, int64_t* top_idx, void* logits, void* ws,
                                hipStream_t stream) {
+  return launch_router_hist(x, w, bias, T, E, D, K, score_func, renorm, renorm_eps, route_scale, top_scores,
+                            top_idx, logits, ws, nullptr, stream);
+}
+
+hipError_t launch_router_hist(const void* x, const void* w, const float* bias, int T, int E, int D, int K,
+                              int score_func, int renorm, float renorm_eps, float route_scale,
+                              float* top_scores, int64_t* top_idx, void* logits, void* ws, int* hist,
+                              hipStream_t stream) {
   if (T == 0) return hipSuccess;
   const int S = router_splits(T, D);
   RouterGemmArgs g;
@@ -336,6 +373,9 @@ hipError_t launch_router_fused(const void* x, const void* w, const float* bias, 
   const int stages = D / RTK;
   g.kstages = (stages + S - 1) / S;
   g.part = (float*)ws;
+  const int nchunks = route_num_chunks((int64_t)T * K);
+  g.zero = hist;
+  g.nzero = hist ? (E + 1) * nchunks : 0;
   hipError_t err;
   if (E <= 32) err = launch_gemm_eb<1>(g, S, stream);
   else if (E <= 64) err = launch_gemm_eb<2>(g, S, stream);
@@ -357,6 +397,9 @@ hipError_t launch_router_fused(const void* x, const void* w, const float* bias, 
   k.scores = top_scores;
   k.idx = top_idx;
   k.logits = (bf16_t*)logits;
+  k.hist = hist;
+  k.nchunks = nchunks;
+  k.chunk = route_chunk_labels();
   const dim3 grid((T + 15) / 16);
   if (E <= 32) hipLaunchKernelGGL(router_topk_partials_kernel<2>, grid, dim3(256), 0, stream, k);
   else if (E <= 64) hipLaunchKernelGGL(router_topk_partials_kernel<4>, grid, dim3(256), 0, stream, k);

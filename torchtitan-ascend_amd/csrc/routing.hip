@@ -22,6 +22,7 @@
 
 #include "../../include/ttamd_moe.h"
 #include "common.h"
+#include "gemm_common.h"
 #include "kernels.h"
 
 namespace ttamd {
@@ -136,13 +137,37 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
   }
 }
 
-template <typename IdxT>
+// Fused-scan form of the rank pass (FUSED = true): `base` is the raw
+// per-chunk histogram, and every workgroup derives the first output position
+// of (bucket b, its chunk c) itself,
+//   base(b, c) = sum_{b' < b} total(b') + sum_{c' < c} hist[b][c'],
+// reading the whole histogram (L2-resident; kFusedScanMax entries at most),
+// which takes the single-workgroup scan launch off the path.  Workgroup 0
+// then also writes counts / offsets, adds the counts to tokens_per_expert
+// (the upstream router's load-balancing accumulator) and builds the grouped
+// GEMMs' tile table of the expert-sorted rows, each when its pointer is set.
+constexpr int kFusedScanMax = 32768;
+constexpr int kBucketsPerThread = (1024 + 1 + kRouteThreads - 1) / kRouteThreads;  // E <= 1024
+
+struct RouteExtras {
+  int* counts;                // int32 [E]
+  int* offsets;               // int32 [E + 1], exclusive
+  float* tokens_per_expert;   // fp32 [E], += counts
+  int4* plan_table;           // tile table (gemm_common.h block_tile_table)
+  int* plan_count;
+  int plan_max_tiles;
+  int plan_max_rows;
+};
+
+template <typename IdxT, bool FUSED>
 __global__ __launch_bounds__(kRouteThreads) void route_rank_kernel(
     const IdxT* __restrict__ labels, const float* __restrict__ scores, int M,
     int E, int nbits, int nchunks, const int* __restrict__ base,
     int* __restrict__ sorted_idx, int* __restrict__ inverse,
-    float* __restrict__ sorted_scores) {
-  extern __shared__ int sh_cnt[];  // [kRouteWaves][E + 1]
+    float* __restrict__ sorted_scores, const RouteExtras x) {
+  // [kRouteWaves][E + 1] wave counters; FUSED: + chunk bases [E + 1],
+  // bucket starts [E + 1] and kRouteWaves + 1 scan ints
+  extern __shared__ int sh_cnt[];
   const int E1 = E + 1;
   const int w = threadIdx.x / kWave, l = lane_id();
   for (int i = threadIdx.x; i < kRouteWaves * E1; i += kRouteThreads) sh_cnt[i] = 0;
@@ -171,9 +196,83 @@ __global__ __launch_bounds__(kRouteThreads) void route_rank_kernel(
     lds_wait();  // the leader's counter update is visible to the next step
   }
   __syncthreads();
+  int* sh_base = sh_cnt + kRouteWaves * E1;
+  if constexpr (FUSED) {
+    int* sh_start = sh_base + E1;
+    int* sh_scan = sh_start + E1;
+    // thread tid owns the consecutive buckets [tid * per, tid * per + per)
+    const int tid = threadIdx.x;
+    const int per = (E1 + kRouteThreads - 1) / kRouteThreads;
+    int tot[kBucketsPerThread], pre[kBucketsPerThread];
+    int mine = 0;
+#pragma unroll
+    for (int i = 0; i < kBucketsPerThread; ++i) {
+      const int b = tid * per + i;
+      tot[i] = pre[i] = 0;
+      if (i < per && b < E1) {
+        const int* row = base + (size_t)b * nchunks;
+        int c = 0;
+        for (; c + 8 <= nchunks; c += 8) {
+          int v[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) v[u] = row[c + u];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            tot[i] += v[u];
+            if (c + u < (int)blockIdx.x) pre[i] += v[u];
+          }
+        }
+        for (; c < nchunks; ++c) {
+          const int v = row[c];
+          tot[i] += v;
+          if (c < (int)blockIdx.x) pre[i] += v;
+        }
+      }
+      mine += tot[i];
+    }
+    // exclusive scan of the per-thread totals over the workgroup
+    const int incl = wave_inclusive_scan(mine);
+    if (l == kWave - 1) sh_scan[w] = incl;
+    __syncthreads();
+    if (tid == 0) {
+      int run = 0;
+      for (int ww = 0; ww < kRouteWaves; ++ww) {
+        const int t = sh_scan[ww];
+        sh_scan[ww] = run;
+        run += t;
+      }
+    }
+    __syncthreads();
+    int start = sh_scan[w] + incl - mine;
+#pragma unroll
+    for (int i = 0; i < kBucketsPerThread; ++i) {
+      const int b = tid * per + i;
+      if (i < per && b < E1) {
+        sh_start[b] = start;
+        sh_base[b] = start + pre[i];
+        if (blockIdx.x == 0) {
+          if (x.offsets) x.offsets[b] = start;
+          if (b < E) {
+            if (x.counts) x.counts[b] = tot[i];
+            if (x.tokens_per_expert) x.tokens_per_expert[b] += (float)tot[i];
+          }
+        }
+        start += tot[i];
+      }
+    }
+    __syncthreads();
+    if (blockIdx.x == 0 && x.plan_table) {
+      auto range = [&](int e, int& r0, int& r1) {
+        r0 = sh_start[e];
+        r1 = sh_start[e + 1];
+      };
+      block_tile_table<kRouteThreads>(range, E, x.plan_max_tiles, x.plan_max_rows, x.plan_table, x.plan_count,
+                                      sh_scan);
+    }
+  }
   // Running base of (wave w, bucket b) = chunk base + counts of earlier waves.
   for (int b = threadIdx.x; b < E1; b += kRouteThreads) {
-    int run = base[(size_t)b * nchunks + blockIdx.x];
+    int run = FUSED ? sh_base[b] : base[(size_t)b * nchunks + blockIdx.x];
 #pragma unroll
     for (int ww = 0; ww < kRouteWaves; ++ww) {
       const int t = sh_cnt[ww * E1 + b];
@@ -255,41 +354,109 @@ hipError_t route_scratch(hipStream_t stream, void** ptr) {
   return hipSuccess;
 }
 
+// counts of the route (after its scan) added into tokens_per_expert
+__global__ __launch_bounds__(256) void accumulate_counts_kernel(const int* __restrict__ counts, int E,
+                                                                float* __restrict__ acc) {
+  for (int e = blockIdx.x * 256 + threadIdx.x; e < E; e += gridDim.x * 256) acc[e] += (float)counts[e];
+}
+
+namespace {
+
+int route_nbits(int E) {
+  int nbits = 0;
+  while ((1 << nbits) <= E) ++nbits;  // bucket values 0..E
+  return nbits;
+}
+
+template <bool FUSED>
+hipError_t launch_rank(const void* labels, bool is64, const float* scores, int M, int E, int nchunks,
+                       const int* hist, int* sorted_idx, int* inverse, float* sorted_scores,
+                       const RouteExtras& x, hipStream_t stream) {
+  const size_t sh = ((size_t)(kRouteWaves + (FUSED ? 2 : 0)) * (E + 1) + (FUSED ? kRouteWaves + 1 : 0)) *
+                    sizeof(int);
+  const int nbits = route_nbits(E);
+  if (is64)
+    hipLaunchKernelGGL((route_rank_kernel<int64_t, FUSED>), dim3(nchunks), dim3(kRouteThreads), sh, stream,
+                       (const int64_t*)labels, scores, M, E, nbits, nchunks, hist, sorted_idx, inverse,
+                       sorted_scores, x);
+  else
+    hipLaunchKernelGGL((route_rank_kernel<int32_t, FUSED>), dim3(nchunks), dim3(kRouteThreads), sh, stream,
+                       (const int32_t*)labels, scores, M, E, nbits, nchunks, hist, sorted_idx, inverse,
+                       sorted_scores, x);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool route_fused_scan(int64_t M, int E) {
+  const int64_t nchunks = (M + kRouteChunk - 1) / kRouteChunk;
+  return (int64_t)(E + 1) * nchunks <= kFusedScanMax;
+}
+
+int route_num_chunks(int64_t M) { return (int)((M + kRouteChunk - 1) / kRouteChunk); }
+
+int route_chunk_labels() { return kRouteChunk; }
+
+hipError_t launch_route_from_hist(const void* labels, bool is64, int M, int E, const float* scores,
+                                  int* counts, int* offsets, int* sorted_idx, int* inverse,
+                                  float* sorted_scores, int* hist, float* tokens_per_expert,
+                                  void* plan, int plan_max_rows, hipStream_t stream) {
+  const int nchunks = route_num_chunks(M);
+  RouteExtras x = {};
+  x.counts = counts;
+  x.offsets = offsets;
+  x.tokens_per_expert = tokens_per_expert;
+  if (plan) {
+    const TileTable tt = tile_table_in(plan);
+    x.plan_table = tt.table;
+    x.plan_count = tt.count;
+    x.plan_max_tiles = max_row_tiles(M, E);
+    x.plan_max_rows = plan_max_rows;
+  }
+  if (M == 0) {  // nothing routed: zero counts / offsets, an empty tile table
+    hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), (size_t)(E + 2) * sizeof(int), stream,
+                       hist, 0, E, 1, 0, counts, offsets);
+    hipError_t err = hipGetLastError();
+    if (err == hipSuccess && plan) err = launch_tile_map(offsets + 1, E, 0, plan_max_rows, plan, stream);
+    return err;
+  }
+  if (route_fused_scan(M, E))
+    return launch_rank<true>(labels, is64, scores, M, E, nchunks, hist, sorted_idx, inverse, sorted_scores, x,
+                             stream);
+  // large histograms: the single-workgroup scan, then the rank pass, the
+  // tile table and the accumulation as separate launches
+  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), (size_t)(E + 2) * sizeof(int), stream,
+                     hist, (E + 1) * nchunks, E, nchunks, M, counts, offsets);
+  hipError_t err = launch_rank<false>(labels, is64, scores, M, E, nchunks, hist, sorted_idx, inverse,
+                                      sorted_scores, RouteExtras{}, stream);
+  if (err == hipSuccess && plan) err = launch_tile_map(offsets + 1, E, M, plan_max_rows, plan, stream);
+  if (err == hipSuccess && tokens_per_expert) {
+    hipLaunchKernelGGL(accumulate_counts_kernel, dim3((E + 255) / 256), dim3(256), 0, stream, counts, E,
+                       tokens_per_expert);
+    err = hipGetLastError();
+  }
+  return err;
+}
+
 hipError_t launch_route(const void* labels, bool is64, int M, int E,
                         const float* scores, int* counts, int* offsets,
                         int* sorted_idx, int* inverse, float* sorted_scores,
                         void* ws, hipStream_t stream) {
-  const int nchunks = (M + kRouteChunk - 1) / kRouteChunk;
+  const int nchunks = route_num_chunks(M);
   int* hist = (int*)ws;
-  int nbits = 0;
-  while ((1 << nbits) <= E) ++nbits;  // bucket values 0..E
-  const size_t sh1 = (size_t)(E + 1) * sizeof(int);
-  const size_t sh2 = (size_t)(E + 2) * sizeof(int);
-  const size_t sh3 = (size_t)kRouteWaves * (E + 1) * sizeof(int);
-  if (M == 0) {
-    hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), sh2, stream,
-                       hist, 0, E, 1, 0, counts, offsets);
-    return hipGetLastError();
+  if (M > 0) {
+    const size_t sh1 = (size_t)(E + 1) * sizeof(int);
+    if (is64)
+      hipLaunchKernelGGL(route_hist_kernel<int64_t>, dim3(nchunks), dim3(kRouteThreads), sh1, stream,
+                         (const int64_t*)labels, M, E, nchunks, hist);
+    else
+      hipLaunchKernelGGL(route_hist_kernel<int32_t>, dim3(nchunks), dim3(kRouteThreads), sh1, stream,
+                         (const int32_t*)labels, M, E, nchunks, hist);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
   }
-  if (is64) {
-    hipLaunchKernelGGL(route_hist_kernel<int64_t>, dim3(nchunks), dim3(kRouteThreads), sh1,
-                       stream, (const int64_t*)labels, M, E, nchunks, hist);
-  } else {
-    hipLaunchKernelGGL(route_hist_kernel<int32_t>, dim3(nchunks), dim3(kRouteThreads), sh1,
-                       stream, (const int32_t*)labels, M, E, nchunks, hist);
-  }
-  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), sh2, stream, hist,
-                     (E + 1) * nchunks, E, nchunks, M, counts, offsets);
-  if (is64) {
-    hipLaunchKernelGGL(route_rank_kernel<int64_t>, dim3(nchunks), dim3(kRouteThreads), sh3,
-                       stream, (const int64_t*)labels, scores, M, E, nbits, nchunks, hist,
-                       sorted_idx, inverse, sorted_scores);
-  } else {
-    hipLaunchKernelGGL(route_rank_kernel<int32_t>, dim3(nchunks), dim3(kRouteThreads), sh3,
-                       stream, (const int32_t*)labels, scores, M, E, nbits, nchunks, hist,
-                       sorted_idx, inverse, sorted_scores);
-  }
-  return hipGetLastError();
+  return launch_route_from_hist(labels, is64, M, E, scores, counts, offsets, sorted_idx, inverse, sorted_scores,
+                                hist, nullptr, nullptr, 0, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -227,12 +227,13 @@ def moe_experts_forward(
 ) -> torch.Tensor:
     """dispatch -> experts -> combine for one GPU; x [T, D], scores/indices [T, K] -> [T, D].
 
-    With autograd off (or nothing requiring grad) the score multiply and the
-    un-permute are fused into the w2 GEMM epilogue.  ``stage_events``, when
-    given (inference path only), receives a (start, end) pair of
-    torch.cuda.Event per stage, recorded on the current stream around the
-    stage's kernels: {"route", "permute", "gemm_w13_swiglu",
-    "gemm_w2_unpermute", "sum_topk"}.
+    With autograd off (or nothing requiring grad) the expert stage is one
+    C-ABI call (ops.experts_forward: both grouped GEMMs on one tile table,
+    the score multiply and the un-permute in the w2 GEMM epilogue).
+    ``stage_events``, when given (inference path only), runs the same kernels
+    one op at a time and receives a (start, end) pair of torch.cuda.Event
+    per stage, recorded on the current stream around the stage's kernels:
+    {"route", "permute", "gemm_w13_swiglu", "gemm_w2_unpermute", "sum_topk"}.
     """
     T, D = x.shape
     K = top_scores.shape[-1]
@@ -252,6 +253,9 @@ def moe_experts_forward(
     mark("route", True)
     offs = r.offs
     xb = x.to(_BF16).contiguous()
+    if not training and ev is None and D % 128 == 0:
+        out = ops.experts_forward(xb, r, _bf16(w13), _bf16(w2), K, score_before_experts, swiglu_limit)
+        return out.to(x.dtype)
     if not training:
         w13b, w2b = _bf16(w13), _bf16(w2)
         if score_before_experts or D < 128:

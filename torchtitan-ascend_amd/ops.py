@@ -78,6 +78,9 @@ class RouteResult:
     sorted_indices: torch.Tensor  # int32 [M]: j-th flat slot in stable expert order
     inverse: torch.Tensor  # int32 [M]: position of flat slot s
     sorted_scores: torch.Tensor | None  # fp32 [M] or None
+    # uint8 tile table of the expert-sorted rows for the forward grouped
+    # GEMMs (router_route builds it; experts_forward reuses it)
+    plan: torch.Tensor | None = None
 
     @property
     def offs(self) -> torch.Tensor:
@@ -168,6 +171,104 @@ def router_fused(
     if return_logits:
         return scores, idx, logits
     return scores, idx
+
+
+def router_route(
+    x: torch.Tensor,
+    w_router: torch.Tensor,
+    top_k: int,
+    score_func: str = "softmax",
+    route_norm: bool = False,
+    route_scale: float = 1.0,
+    expert_bias: torch.Tensor | None = None,
+    norm_eps: float = 1e-20,
+    tokens_per_expert: torch.Tensor | None = None,
+    with_inverse: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor, RouteResult]:
+    """Router forward + dispatch order in one C-ABI call (ttamd_router_route):
+    the picks of `router_fused`, then the histogram and stable order of
+    `route` over them, plus the grouped GEMMs' tile table (RouteResult.plan).
+    tokens_per_expert (fp32 [E], optional) is incremented by the counts, as
+    upstream's router.tokens_per_expert buffer is.  Returns (top_scores
+    fp32 [T, K], selected_experts_indices int64 [T, K], RouteResult with
+    sorted_scores = top_scores.view(-1)[sorted_indices])."""
+    dev = _gpu("x", x)
+    x = _want("x", x.reshape(-1, x.shape[-1]), _BF16)
+    w_router = _want("w_router", w_router, _BF16)
+    T, D = x.shape
+    E, D2 = w_router.shape
+    if D2 != D:
+        raise ValueError(f"w_router must be [E, {D}], got {tuple(w_router.shape)}")
+    funcs = {"softmax": 0, "sigmoid": 1}
+    if score_func not in funcs:
+        raise ValueError(f"score_func must be one of {sorted(funcs)}")
+    if expert_bias is not None:
+        _same_device(dev, expert_bias=expert_bias)
+        expert_bias = expert_bias.float().contiguous()
+        if expert_bias.shape != (E,):
+            raise ValueError("expert_bias must be [E]")
+    if tokens_per_expert is not None:
+        _same_device(dev, tokens_per_expert=tokens_per_expert)
+        if tokens_per_expert.dtype != torch.float32 or tokens_per_expert.shape != (E,) or \
+                not tokens_per_expert.is_contiguous():
+            raise ValueError("tokens_per_expert must be a contiguous fp32 [E] tensor (updated in place)")
+    M = T * top_k
+    lib = _lib.load()
+    scores = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+    idx = torch.empty(T, top_k, dtype=torch.int64, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    sorted_idx = torch.empty(M, dtype=torch.int32, device=dev)
+    inverse = torch.empty(M, dtype=torch.int32, device=dev) if with_inverse else None
+    sorted_scores = torch.empty(M, dtype=torch.float32, device=dev)
+    plan = _ws(lib.ttamd_gemm_workspace_bytes(M, E), dev)
+    ws = _ws(lib.ttamd_router_route_workspace_bytes(T, E, D, top_k), dev)
+    _lib.call(
+        "ttamd_router_route", _p(x), _p(w_router), _p(expert_bias), T, E, D, top_k, funcs[score_func],
+        int(bool(route_norm)), float(norm_eps), float(route_scale), _p(scores), _p(idx), _p(counts), _p(offsets),
+        _p(sorted_idx), _p(inverse), _p(sorted_scores), _p(tokens_per_expert), _p(plan), plan.numel(), _p(ws),
+        ws.numel(), _stream(dev),
+    )
+    return scores, idx, RouteResult(counts, offsets, sorted_idx, inverse, sorted_scores, plan)
+
+
+def experts_forward(
+    x: torch.Tensor,
+    r: RouteResult,
+    w13: torch.Tensor,
+    w2: torch.Tensor,
+    top_k: int,
+    score_before_experts: bool,
+    swiglu_limit: float | None = None,
+) -> torch.Tensor:
+    """The expert stage of the inference forward in one C-ABI call
+    (ttamd_moe_experts_forward): dispatch -> w13 + SwiGLU -> w2 + score ->
+    combine (npu_gmm.py:100-110 with :21-40) on the routing `r` (from
+    `route` or `router_route`; r.sorted_scores must be set).  Both grouped
+    GEMMs use r.plan when present.  x bf16 [T, D] -> out bf16 [T, D]."""
+    dev = _gpu("x", x)
+    x = _want("x", x, _BF16)
+    w13 = _want("w13", w13, _BF16)
+    w2 = _want("w2", w2, _BF16)
+    T, D = x.shape
+    E, H2, D2 = w13.shape
+    if D2 != D or H2 % 2 or tuple(w2.shape) != (E, D, H2 // 2):
+        raise ValueError(f"w13 must be [E, 2H, {D}] and w2 [E, {D}, H]; got {tuple(w13.shape)}, {tuple(w2.shape)}")
+    H = H2 // 2
+    if r.sorted_scores is None:
+        raise ValueError("experts_forward needs the routing scores (route(..., scores))")
+    if r.sorted_indices.numel() != T * top_k:
+        raise ValueError("routing does not match T * top_k rows")
+    lib = _lib.load()
+    out = torch.empty(T, D, dtype=_BF16, device=dev)
+    ws = _ws(lib.ttamd_moe_experts_forward_workspace_bytes(T, D, H, E, top_k, int(bool(score_before_experts))), dev)
+    plan = r.plan
+    _lib.call(
+        "ttamd_moe_experts_forward", _p(x), T, D, H, E, top_k, _p(r.sorted_indices), _p(r.offs.contiguous()),
+        _p(r.sorted_scores), int(bool(score_before_experts)), _limit(swiglu_limit), _p(w13), _p(w2), _p(out),
+        _p(plan), 0 if plan is None else plan.numel(), _p(ws), ws.numel(), _stream(dev),
+    )
+    return out
 
 
 def route(
