@@ -183,15 +183,19 @@ def main():
         w2p = w2.clone().requires_grad_(True)
         dout = torch.randn(T, D, device=dev).to(torch.bfloat16)
         xg = x.clone().requires_grad_(True)
+        w_router_p = w_router.clone().requires_grad_(True)
         if shared:
             sw13.requires_grad_(True)
             sw2.requires_grad_(True)
 
         def step(ev=None):
-            # a training step starts from cleared gradients (zero_grad(set_to_none=True))
-            w13p.grad = w2p.grad = xg.grad = None
-            scores, idx = router()
-            scores = scores.detach().requires_grad_(True)
+            # a training step starts from cleared gradients (zero_grad(set_to_none=True));
+            # the router is differentiated with the layer (dx and the gate weight's gradient)
+            w13p.grad = w2p.grad = xg.grad = w_router_p.grad = None
+            if zipf_idx is not None:
+                scores, idx = zipf_scores.clone().requires_grad_(True), zipf_idx
+            else:
+                scores, idx = F.router(xg, w_router_p, K, cfg["router"], cfg["norm"])
             out = F.moe_experts_forward(xg, scores, idx, w13p, w2p, E, cfg["score_before"])
             if shared:
                 sw13.grad = sw2.grad = None

@@ -96,6 +96,37 @@ int ttamd_router_fused(const void* x, const void* w_router,
                        size_t workspace_bytes, void* stream);
 
 /*
+ * Router backward: the autograd of the router forward above.
+ * Replaces the backward torch autograd runs through upstream
+ * TokenChoiceTopKRouter.forward (closed form
+ * torchtitanturbo/models/qwen3_5/model.py:752-766: gate nn.Linear in bf16,
+ * softmax / sigmoid in fp32, topk / gather, renorm, route_scale).
+ *   g_k    = route_scale * grad_top_scores[t, k]
+ *   renorm: S = sum_k s[idx_k] + eps; ds[idx_k] = g_k / S
+ *           + sum_j (-g_j s[idx_j] / S^2); else ds[idx_k] = g_k (0 elsewhere)
+ *   softmax: dz = (ds - <ds, s>) * s;  sigmoid: dz = ds * (1 - s) * s
+ *   dlogits = bf16(dz)  (the gradient of the bf16 logits)
+ *   grad_x [T, D] bf16 = dlogits . w_router          (nullable)
+ *   grad_w_router [E, D] = dlogits^T . x              (nullable; fp32 when
+ *                                                      grad_w_is_fp32, else bf16)
+ * s is recomputed from logits (bf16 [T, E], the forward's logits_out).
+ * expert_bias only steers the selection and has no gradient here.
+ * D % 128 == 0; other limits as ttamd_router_fused.  workspace:
+ * ttamd_router_backward_workspace_bytes.
+ */
+size_t ttamd_router_backward_workspace_bytes(int64_t num_tokens,
+                                             int num_experts, int64_t dim);
+int ttamd_router_backward(const float* grad_top_scores,
+                          const int64_t* top_indices, const void* logits,
+                          const void* x, const void* w_router,
+                          int64_t num_tokens, int num_experts, int64_t dim,
+                          int topk, int score_func, int renorm,
+                          float renorm_eps, float route_scale, void* grad_x,
+                          void* grad_w_router, int grad_w_is_fp32,
+                          void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/*
  * Router + dispatch order in one call: the router of ttamd_router_fused,
  * then the histogram and stable order of ttamd_moe_route over its picks
  * (selected_experts_indices.view(-1)), with no round trip between them.

@@ -36,6 +36,9 @@ PINNED = {
                          "sigmoid(shared_expert_gate), expert_output + shared, model.py:794-809); a dropped gate "
                          "fails it",
     "moe_backward": "torch autograd of a torch fp32 restatement (golden); central finite differences",
+    "router_backward": "torch CPU autograd of the upstream router op sequence (bf16 F.linear, fp32 softmax / "
+                       "sigmoid, topk, renorm, route_scale) golden: dlogits, dx, dw; central finite differences "
+                       "of router_forward_f64 (a dropped renorm term or a wrong softmax Jacobian fails them)",
     "grouped_dgrad / grouped_wgrad": "through moe_backward's autograd golden (they are its dx / dW steps); "
                                      "brute-force triple loop on tiny shapes",
     "swiglu_backward": "through moe_backward (above); finite differences of swiglu on clamped and unclamped values",
@@ -208,6 +211,72 @@ def router_topk(logits: np.ndarray, top_k: int, score_func: str = "softmax", rou
         top = top / (top.sum(axis=-1, keepdims=True) + norm_eps)
     top = top * route_scale
     return top.astype(np.float32), order.astype(np.int64)
+
+
+def router_scores(logits: np.ndarray, score_func: str) -> np.ndarray:
+    """fp32 expert scores of the router: softmax over experts or sigmoid
+    (models/qwen3_5/model.py:758; UPSTREAM sigmoid)."""
+    z = np.asarray(logits, np.float32)
+    if score_func == "softmax":
+        m = z.max(axis=-1, keepdims=True)
+        e = np.exp((z - m).astype(np.float64))
+        return (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+    if score_func == "sigmoid":
+        return (1.0 / (1.0 + np.exp(-z.astype(np.float64)))).astype(np.float32)
+    raise ValueError(score_func)
+
+
+def router_backward(x: np.ndarray, w_router: np.ndarray, logits: np.ndarray, idx: np.ndarray,
+                    grad_top: np.ndarray, score_func: str = "softmax", route_norm: bool = False,
+                    route_scale: float = 1.0, norm_eps: float = 1e-20, round_bf16: bool = True):
+    """Autograd of the router forward (UPSTREAM TokenChoiceTopKRouter; closed
+    form models/qwen3_5/model.py:757-765): logits = x w^T (bf16 Linear),
+    s = softmax / sigmoid(logits) in fp32, top = s[idx] (renormalised by
+    sum + eps when route_norm) * route_scale.  Given d(top) [T, K] and the
+    picks idx (selection has no gradient; expert_bias only steers it):
+        ds[idx_k] = g_k / S - sum_j g_j s_j / S^2  (renorm),  g_k otherwise
+        dz = (ds - <ds, s>) s  (softmax)  or  ds (1 - s) s  (sigmoid)
+        dlogits = bf16(dz)   (the gradient of the bf16 logits)
+        dx = dlogits w,  dw = dlogits^T x   (float64 accumulation)
+    Returns (dx, dw, dlogits) in fp32; with round_bf16=False nothing is
+    rounded (the smooth function finite differences see)."""
+    s = router_scores(logits, score_func).astype(np.float64)
+    T, E = s.shape
+    idx = np.asarray(idx, np.int64).reshape(T, -1)
+    g = np.asarray(grad_top, np.float64).reshape(T, -1) * route_scale
+    picked = np.take_along_axis(s, idx, axis=-1)
+    if route_norm:
+        S = picked.sum(-1, keepdims=True) + norm_eps
+        ds_k = g / S - (g * picked).sum(-1, keepdims=True) / (S * S)
+    else:
+        ds_k = g
+    ds = np.zeros((T, E))
+    np.add.at(ds, (np.arange(T)[:, None], idx), ds_k)
+    if score_func == "softmax":
+        dz = (ds - (ds * s).sum(-1, keepdims=True)) * s
+    else:
+        dz = ds * (1.0 - s) * s
+    dlog = bf16_round(dz.astype(np.float32)) if round_bf16 else dz
+    dx = np.asarray(dlog, np.float64) @ np.asarray(w_router, np.float64)
+    dw = np.asarray(dlog, np.float64).T @ np.asarray(x, np.float64)
+    return dx.astype(np.float32), dw.astype(np.float32), np.asarray(dlog, np.float32)
+
+
+def router_forward_f64(x: np.ndarray, w_router: np.ndarray, idx: np.ndarray, score_func: str,
+                       route_norm: bool, route_scale: float, norm_eps: float = 1e-20) -> np.ndarray:
+    """The router forward in float64 with fixed picks and no bf16 rounding:
+    the smooth function router_backward(round_bf16=False) differentiates
+    (for finite-difference checks)."""
+    z = np.asarray(x, np.float64) @ np.asarray(w_router, np.float64).T
+    if score_func == "softmax":
+        e = np.exp(z - z.max(-1, keepdims=True))
+        s = e / e.sum(-1, keepdims=True)
+    else:
+        s = 1.0 / (1.0 + np.exp(-z))
+    top = np.take_along_axis(s, np.asarray(idx, np.int64), axis=-1)
+    if route_norm:
+        top = top / (top.sum(-1, keepdims=True) + norm_eps)
+    return top * route_scale
 
 
 # ---------------------------------------------------------------------------

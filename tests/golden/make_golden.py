@@ -129,6 +129,34 @@ def router_gate_case():
     _save("gate_linear", x=x.float().numpy(), w=w.float().numpy(), logits=logits.float().numpy())
 
 
+def router_backward_cases():
+    """Autograd of the upstream router's op sequence on CPU torch
+    (models/qwen3_5/model.py:757-765 closed form): bf16 gate Linear, fp32
+    softmax / sigmoid, topk, optional renorm (+1e-20), route_scale; d(top)
+    random.  Saves the bf16 logits' gradient and dx, dw."""
+    g = torch.Generator().manual_seed(11)
+    T, D, E = 40, 128, 24
+    x0 = _bf16(torch.randn(T, D, generator=g))
+    w0 = _bf16(torch.randn(E, D, generator=g) * 0.05)
+    for func, K, norm, scale in (("softmax", 4, True, 1.0), ("softmax", 2, False, 2.5), ("sigmoid", 1, False, 1.0),
+                                 ("sigmoid", 3, True, 1.5)):
+        x = x0.clone().requires_grad_(True)
+        w = w0.clone().requires_grad_(True)
+        logits = F.linear(x, w)
+        logits.retain_grad()
+        s = torch.softmax(logits.float(), dim=-1) if func == "softmax" else torch.sigmoid(logits.float())
+        top, idx = torch.topk(s, K, dim=-1)
+        if norm:
+            top = top / (top.sum(dim=-1, keepdim=True) + 1e-20)
+        top = top * scale
+        gtop = torch.randn(T, K, generator=g)
+        top.backward(gtop)
+        _save(f"backward_router_{func}_k{K}_{'norm' if norm else 'raw'}", x=x0.float().numpy(), w=w0.float().numpy(),
+              logits=logits.detach().float().numpy(), idx=idx.numpy(), grad_top=gtop.numpy(),
+              route_scale=np.float32(scale), dlogits=logits.grad.float().numpy(), dx=x.grad.float().numpy(),
+              dw=w.grad.float().numpy())
+
+
 def experts_cases():
     """The reference's op sequence (npu_gmm.py:29-38) on CPU torch, bf16."""
     g = torch.Generator().manual_seed(3)
@@ -292,6 +320,7 @@ if __name__ == "__main__":
     permute_cases()
     router_cases()
     router_gate_case()
+    router_backward_cases()
     shared_expert_case()
     experts_cases()
     layer_cases()

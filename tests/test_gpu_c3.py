@@ -12,7 +12,9 @@ Checked (tolerance: the path's 2e-2, norm-wise AND per row / per slice):
   * dW13 and dW2 in full for two experts (oracle on those experts' rows);
   * for every other expert, ~32 gate rows (+ their up rows) of dW13 and ~32
     columns of dW2, one or two in each of its 256-wide n / k tiles;
-  * the shared expert's dW13 rows / dW2 columns likewise.
+  * the shared expert's dW13 rows / dW2 columns likewise;
+  * the router (differentiated with the layer): its share of dX on the
+    sampled tokens and the router weight gradient dW_r [E, D].
 Reference: autograd through torch._grouped_mm (npu_gmm.py:21-40) and the
 unpermute (npu_permute.py:35-53); shared expert as models/qwen3_5/model.py
 :794-809 without the gate (UPSTREAM Llama4)."""
@@ -73,10 +75,14 @@ def test_c3_llama4_scout_fwd_bwd_full_size(pkg, ops):
     dout = torch.randn(T, D, device=DEV).to(torch.bfloat16)
 
     announce("C3 full size: router + layer forward + backward on the GPU")
-    with torch.no_grad():
-        scores, idx = ops.router_fused(x, w_router, K, "sigmoid", False)
-    sc = scores.detach().clone().requires_grad_(True)
+    # the router is part of the differentiated graph: x and w_router get its
+    # gradient too (scores.grad is kept to check d(top_scores))
     xg = x.clone().requires_grad_(True)
+    wr = w_router.clone().requires_grad_(True)
+    sc, idx = F.router(xg, wr, K, "sigmoid", False)
+    sc.retain_grad()
+    with torch.no_grad():
+        _, _, logits = ops.router_fused(x, w_router, K, "sigmoid", False, return_logits=True)
     out = m(xg.view(1, T, D), sc, idx)
     out = F.shared_expert_combine(out, xg, sw13, sw2)
     out.backward(dout)
@@ -146,8 +152,16 @@ def test_c3_llama4_scout_fwd_bwd_full_size(pkg, ops):
 
     ref_out = O.bf16_round(routed_y + sh_y)
     assert_close(to_np(out[tt]), ref_out, TOL, "layer output (sampled tokens)")
-    assert_close(to_np(xg.grad[tt]), dx_routed + sh["dx"], TOL, "dX (sampled tokens)")
     assert_dot_close(to_np(sc.grad[tt]), ds, ds_abs, TOL, "d(top_scores) (sampled tokens)")
+    # the router's share of dX on the sampled tokens, from the oracle's d(top_scores)
+    lg = to_np(logits)
+    dx_router, _, _ = O.router_backward(x_s, to_np(w_router), lg[tok], idx_np[tok], ds, "sigmoid", False, 1.0)
+    assert_close(to_np(xg.grad[tt]), dx_routed + sh["dx"] + dx_router, TOL, "dX (sampled tokens)")
+
+    announce("C3 full size: router weight gradient")
+    # dW_r over every token, from the GPU's d(top_scores) (checked on the samples above)
+    _, dwr, _ = O.router_backward(to_np(x), to_np(w_router), lg, idx_np, to_np(sc.grad), "sigmoid", False, 1.0)
+    assert_close(to_np(wr.grad), dwr, TOL, "router dW")
 
     announce("C3 full size: shared expert weight gradients")
     gr = _spread(H, 32, rng)

@@ -34,6 +34,12 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i64, _i32, _i32, _i32, _f32, _f32, _c_void_p, _c_void_p,
          _c_void_p, _c_void_p, _sz, _c_void_p],
     ),
+    "ttamd_router_backward_workspace_bytes": (_sz, [_i64, _i32, _i64]),
+    "ttamd_router_backward": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i64, _i32, _i32, _i32, _f32, _f32,
+         _c_void_p, _c_void_p, _i32, _c_void_p, _sz, _c_void_p],
+    ),
     "ttamd_router_route_workspace_bytes": (_sz, [_i64, _i32, _i64, _i32]),
     "ttamd_router_route": (
         _i32,

@@ -204,6 +204,39 @@ int ttamd_moe_route_noalloc(const void* labels, int labels_are_int64, int64_t nu
                    fn);
 }
 
+size_t ttamd_router_backward_workspace_bytes(int64_t num_tokens, int num_experts, int64_t dim) {
+  if (num_tokens < 0 || num_experts < 1 || dim < 1) return 0;
+  return ttamd::router_backward_workspace_bytes(num_tokens, num_experts, dim);
+}
+
+int ttamd_router_backward(const float* grad_top_scores, const int64_t* top_indices, const void* logits,
+                          const void* x, const void* w_router, int64_t num_tokens, int num_experts, int64_t dim,
+                          int topk, int score_func, int renorm, float renorm_eps, float route_scale, void* grad_x,
+                          void* grad_w_router, int grad_w_is_fp32, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  const char* fn = "ttamd_router_backward";
+  REQUIRE(num_tokens >= 0 && num_tokens <= (1 << 24), "%s: num_tokens out of range", fn);
+  REQUIRE(num_experts >= 1 && num_experts <= 256, "%s: num_experts must be in [1, 256]", fn);
+  REQUIRE(topk >= 1 && topk <= 16 && topk <= num_experts, "%s: topk must be in [1, min(16, E)]", fn);
+  REQUIRE(score_func == TTAMD_SCORE_SOFTMAX || score_func == TTAMD_SCORE_SIGMOID,
+          "%s: unknown score_func %d", fn, score_func);
+  REQUIRE(dim >= 128 && dim % 128 == 0 && dim <= (1 << 20), "%s: dim must be a positive multiple of 128", fn);
+  if (num_tokens == 0) return TTAMD_OK;
+  REQUIRE(grad_top_scores && top_indices && logits && w_router, "%s: null pointer argument", fn);
+  REQUIRE(grad_w_router == nullptr || x != nullptr, "%s: the weight gradient needs x", fn);
+  REQUIRE(aligned16(w_router), "%s: w_router must be 16-byte aligned", fn);
+  if (x) TRY(check_rows(fn, "x", x, num_tokens, dim));
+  if (grad_x) TRY(check_rows(fn, "grad_x", grad_x, num_tokens, dim));
+  if (grad_w_router) REQUIRE(aligned16(grad_w_router), "%s: grad_w_router must be 16-byte aligned", fn);
+  REQUIRE(num_tokens * dim * 2 <= (int64_t)0xffffffffLL, "%s: x must stay below 4 GiB", fn);
+  TRY(check_ws(fn, workspace, workspace_bytes, ttamd::router_backward_workspace_bytes(num_tokens, num_experts, dim)));
+  return check_hip(ttamd::launch_router_backward(grad_top_scores, top_indices, logits, x, w_router, (int)num_tokens,
+                                                 num_experts, (int)dim, topk, score_func, renorm, renorm_eps,
+                                                 route_scale, grad_x, grad_w_router, grad_w_is_fp32 != 0, workspace,
+                                                 (hipStream_t)stream),
+                   fn);
+}
+
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 size_t ttamd_router_route_workspace_bytes(int64_t num_tokens, int num_experts, int64_t dim, int topk) {

@@ -66,6 +66,14 @@ hipError_t launch_router_hist(const void* x, const void* w, const float* bias, i
                               float* top_scores, int64_t* top_idx, void* logits, void* ws, int* hist,
                               hipStream_t stream);
 
+// Router backward: d(top_scores) -> d(logits) -> dx (bf16 [T, D], nullable)
+// and dW_r ([E, D], fp32 or bf16, nullable).
+size_t router_backward_workspace_bytes(int64_t T, int E, int64_t D);
+hipError_t launch_router_backward(const float* grad, const int64_t* idx, const void* logits, const void* x,
+                                  const void* w, int T, int E, int D, int K, int score_func, int renorm,
+                                  float renorm_eps, float route_scale, void* dx, void* dw, bool dw_fp32,
+                                  void* ws, hipStream_t stream);
+
 // gemm.hip
 int gemm_max_qtiles(int M, int E);
 size_t gemm_workspace_bytes(int64_t M, int E);

@@ -315,6 +315,137 @@ __global__ __launch_bounds__(256) void router_topk_partials_kernel(const RouterT
   }
 }
 
+// ---------------------------------------------------------------------------
+// Router backward, elementwise part: d(top_scores) [T, K] -> d(logits) bf16.
+// Autograd of the upstream router's op sequence (closed form
+// models/qwen3_5/model.py:757-765): top_scores = route_scale * (s[idx] /
+// (sum_k s[idx_k] + eps) if renorm else s[idx]), s = softmax / sigmoid of
+// the bf16 logits in fp32; the gradient reaches the logits cast back to
+// bf16 (the Linear's dtype).  Each step in the order torch's backward
+// formulas take it:
+//   g_k   = route_scale * grad_top[k]
+//   renorm: gd = sum_k (-g_k * s_k / (S * S)); ds_k = g_k / S + gd
+//   softmax: dz = (ds - sum_e ds_e s_e) * s;  sigmoid: dz = ds * (1 - s) * s
+// s is recomputed from the logits with the forward kernel's arithmetic.
+// 16 lanes per token (the forward's lane -> expert map); columns E..ldd-1
+// of the output (padding for the GEMMs that follow) are zero.
+struct RouterBwdArgs {
+  const bf16_t* logits;  // [T, E]
+  const int64_t* idx;    // [T, K]
+  const float* grad;     // [T, K]
+  int T, E, K;
+  int score_func, renorm;
+  float eps, route_scale;
+  bf16_t* dlogits;  // [T, ldd]
+  int ldd;
+};
+
+template <int PL>
+__global__ __launch_bounds__(256) void router_backward_kernel(const RouterBwdArgs a) {
+  constexpr int G = PL < 4 ? PL : 4;
+  const int gi = threadIdx.x & 15;
+  const int t = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const bool valid = t < a.T;
+  const int tt = valid ? t : a.T - 1;
+  auto eid = [&](int m) { return G * gi + m % G + 16 * G * (m / G); };
+  float sc[PL];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int m = 0; m < PL; ++m) {
+    const int e = eid(m);
+    const float z = (e < a.E) ? bf16_to_f32(a.logits[(int64_t)tt * a.E + e]) : -INFINITY;
+    sc[m] = z;
+    mx = fmaxf(mx, z);
+  }
+  if (a.score_func == 0) {
+    mx = row16_max(mx);
+    float sum = 0.f;
+#pragma unroll
+    for (int m = 0; m < PL; ++m) {
+      const int e = eid(m);
+      sc[m] = (e < a.E) ? expf(sc[m] - mx) : 0.f;
+      sum += sc[m];
+    }
+    sum = row16_sum(sum);
+#pragma unroll
+    for (int m = 0; m < PL; ++m) sc[m] = sc[m] / sum;
+  } else {
+#pragma unroll
+    for (int m = 0; m < PL; ++m) sc[m] = 1.f / (1.f + expf(-sc[m]));
+  }
+  // picked experts, their scores (broadcast over the 16 lanes) and grads
+  float ds[PL];
+#pragma unroll
+  for (int m = 0; m < PL; ++m) ds[m] = 0.f;
+  float S = 0.f, gd = 0.f;
+  if (a.renorm) {
+    for (int k = 0; k < a.K; ++k) {
+      const int ek = (int)a.idx[(int64_t)tt * a.K + k];
+      float v = 0.f;
+#pragma unroll
+      for (int m = 0; m < PL; ++m)
+        if (eid(m) == ek) v = sc[m];
+      S += row16_sum(v);  // one lane holds s[ek]; picked in k order, as the forward sums them
+    }
+    S += a.eps;
+    for (int k = 0; k < a.K; ++k) {
+      const int ek = (int)a.idx[(int64_t)tt * a.K + k];
+      const float g = a.grad[(int64_t)tt * a.K + k] * a.route_scale;
+      float v = 0.f;
+#pragma unroll
+      for (int m = 0; m < PL; ++m)
+        if (eid(m) == ek) v = sc[m];
+      gd += -g * row16_sum(v) / (S * S);
+    }
+  }
+  for (int k = 0; k < a.K; ++k) {
+    const int ek = (int)a.idx[(int64_t)tt * a.K + k];
+    const float g = a.grad[(int64_t)tt * a.K + k] * a.route_scale;
+    const float d = a.renorm ? g / S + gd : g;
+#pragma unroll
+    for (int m = 0; m < PL; ++m)
+      if (eid(m) == ek) ds[m] += d;
+  }
+  if (a.score_func == 0) {
+    float dot = 0.f;
+#pragma unroll
+    for (int m = 0; m < PL; ++m) dot += ds[m] * sc[m];
+    dot = row16_sum(dot);
+#pragma unroll
+    for (int m = 0; m < PL; ++m) ds[m] = (ds[m] - dot) * sc[m];
+  } else {
+#pragma unroll
+    for (int m = 0; m < PL; ++m) ds[m] = ds[m] * (1.f - sc[m]) * sc[m];
+  }
+  if (!valid) return;
+  bf16_t* row = a.dlogits + (int64_t)t * a.ldd;
+#pragma unroll
+  for (int m = 0; m < PL; ++m) {
+    const int e = eid(m);
+    if (e < a.E) row[e] = (bf16_t)f32_to_bf16(ds[m]);
+  }
+  for (int e = a.E + gi; e < a.ldd; e += 16) row[e] = 0;
+}
+
+// w_pad [ldd rows][D] = w_router rows, then zero rows; offs1[0] = T (one
+// expert owning every token row, for the padded GEMMs).
+__global__ __launch_bounds__(256) void router_pad_kernel(const uint4* __restrict__ w, int E, int ldd, int cpr,
+                                                         uint4* __restrict__ w_pad, int* offs1, int T) {
+  const int total = ldd * cpr;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256)
+    w_pad[i] = (i / cpr < E) ? w[i] : make_uint4(0, 0, 0, 0);
+  if (blockIdx.x == 0 && threadIdx.x == 0) offs1[0] = T;
+}
+
+// dw[E][D] (fp32 or bf16) = the first E rows of the padded fp32 gradient.
+__global__ __launch_bounds__(256) void router_dw_copy_kernel(const float* __restrict__ src, int n, void* dst,
+                                                             int fp32) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+    if (fp32) ((float*)dst)[i] = src[i];
+    else ((bf16_t*)dst)[i] = (bf16_t)f32_to_bf16(src[i]);
+  }
+}
+
 template <int EB>
 hipError_t launch_gemm_eb(const RouterGemmArgs& a, int S, hipStream_t stream) {
   constexpr int lds = router_nst<EB>() * (RT + 32 * EB) * 128;
@@ -409,5 +540,82 @@ hipError_t launch_router_hist(const void* x, const void* w, const float* bias, i
 }
 
 static_assert(kRouterMaxE == 256, "EB = 8 covers 256 experts");
+
+// ---------------------------------------------------------------------------
+// Router backward: d(logits) (kernel above), then dx = dlogits . W_r and
+// dW_r = dlogits^T . x on the grouped GEMM kernels as one expert, with the
+// expert count padded to a multiple of 128 (zero logit-gradient columns and
+// zero weight rows contribute nothing).
+// ---------------------------------------------------------------------------
+static int router_pad_e(int E) { return (E + 127) & ~127; }
+static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+size_t router_backward_workspace_bytes(int64_t T, int E, int64_t D) {
+  const int64_t P = router_pad_e(E);
+  return al256((size_t)T * P * 2) + al256((size_t)P * D * 2) + al256((size_t)P * D * 4) + al256(16) +
+         al256(gemm_workspace_bytes(T, 1));
+}
+
+hipError_t launch_router_backward(const float* grad, const int64_t* idx, const void* logits, const void* x,
+                                  const void* w, int T, int E, int D, int K, int score_func, int renorm,
+                                  float renorm_eps, float route_scale, void* dx, void* dw, bool dw_fp32,
+                                  void* ws, hipStream_t stream) {
+  if (T == 0) return hipSuccess;
+  const int P = router_pad_e(E);
+  char* p = (char*)ws;
+  bf16_t* dlog = (bf16_t*)p;
+  p += al256((size_t)T * P * 2);
+  bf16_t* w_pad = (bf16_t*)p;
+  p += al256((size_t)P * D * 2);
+  float* dw_pad = (float*)p;
+  p += al256((size_t)P * D * 4);
+  int* offs1 = (int*)p;
+  p += al256(16);
+  void* gws = p;
+
+  RouterBwdArgs b;
+  b.logits = (const bf16_t*)logits;
+  b.idx = idx;
+  b.grad = grad;
+  b.T = T;
+  b.E = E;
+  b.K = K;
+  b.score_func = score_func;
+  b.renorm = renorm;
+  b.eps = renorm_eps;
+  b.route_scale = route_scale;
+  b.dlogits = dlog;
+  b.ldd = P;
+  const dim3 grid((T + 15) / 16);
+  if (E <= 32) hipLaunchKernelGGL(router_backward_kernel<2>, grid, dim3(256), 0, stream, b);
+  else if (E <= 64) hipLaunchKernelGGL(router_backward_kernel<4>, grid, dim3(256), 0, stream, b);
+  else if (E <= 128) hipLaunchKernelGGL(router_backward_kernel<8>, grid, dim3(256), 0, stream, b);
+  else hipLaunchKernelGGL(router_backward_kernel<16>, grid, dim3(256), 0, stream, b);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  const int cpr = D / 8;
+  const int pg = min(2048, (P * cpr + 255) / 256);
+  hipLaunchKernelGGL(router_pad_kernel, dim3(pg), dim3(256), 0, stream, (const uint4*)w, E, P, cpr, (uint4*)w_pad,
+                     offs1, T);
+  if ((err = hipGetLastError()) != hipSuccess) return err;
+  if (dx) {
+    // dx[t][d] = sum_e dlogits[t][e] w[e][d]: dgrad with the weight [1][P][D]
+    if ((err = launch_grouped_mm_dgrad(dlog, w_pad, offs1, T, 1, P, D, dx, gws, stream)) != hipSuccess) return err;
+  }
+  if (dw) {
+    // dw[e][d] = sum_t dlogits[t][e] x[t][d]: wgrad over the one expert
+    const bool direct = (P == E) && dw_fp32;
+    if ((err = launch_grouped_mm_wgrad(dlog, x, offs1, T, 1, P, D, direct ? dw : (void*)dw_pad, true, stream)) !=
+        hipSuccess)
+      return err;
+    if (!direct) {
+      const int n = E * D;
+      hipLaunchKernelGGL(router_dw_copy_kernel, dim3(min(2048, (n + 255) / 256)), dim3(256), 0, stream, dw_pad, n,
+                         dw, dw_fp32 ? 1 : 0);
+      err = hipGetLastError();
+    }
+  }
+  return err;
+}
 
 }  // namespace ttamd

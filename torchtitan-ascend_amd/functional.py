@@ -27,6 +27,63 @@ def _bf16(w: torch.Tensor) -> torch.Tensor:
     return w if w.dtype == _BF16 else w.to(_BF16)
 
 
+class RouterFn(torch.autograd.Function):
+    """Router forward (gate Linear in bf16 + fp32 softmax / sigmoid + top-k +
+    renorm, UPSTREAM TokenChoiceTopKRouter; closed form
+    torchtitanturbo/models/qwen3_5/model.py:752-766) with its backward on the
+    HIP kernels: d(top_scores) -> d(logits) -> dx, dW_r.  The expert ids
+    carry no gradient."""
+
+    @staticmethod
+    def forward(ctx, x, w_router, top_k, score_func, route_norm, route_scale, expert_bias, norm_eps):
+        shape = x.shape
+        xb = x.reshape(-1, shape[-1]).to(_BF16).contiguous()
+        wb = _bf16(w_router).contiguous()
+        scores, idx, logits = ops.router_fused(xb, wb, top_k, score_func, route_norm, route_scale, expert_bias,
+                                               norm_eps, return_logits=True)
+        ctx.save_for_backward(xb, wb, idx, logits)
+        ctx.cfg = (score_func, route_norm, route_scale, norm_eps)
+        ctx.x_shape, ctx.x_dtype, ctx.w_dtype = shape, x.dtype, w_router.dtype
+        ctx.mark_non_differentiable(idx)
+        return scores, idx
+
+    @staticmethod
+    def backward(ctx, g_scores, _g_idx):
+        xb, wb, idx, logits = ctx.saved_tensors
+        func, norm, scale, eps = ctx.cfg
+        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if g_scores is None or not (need_dx or need_dw):
+            return (None,) * 8
+        dx, dw = ops.router_backward(
+            g_scores, idx, logits, xb, wb, func, norm, scale, eps, need_dx, need_dw,
+            torch.float32 if ctx.w_dtype != _BF16 else _BF16,
+        )
+        if dx is not None:
+            dx = dx.view(ctx.x_shape).to(ctx.x_dtype)
+        if dw is not None:
+            dw = dw.to(ctx.w_dtype)
+        return dx, dw, None, None, None, None, None, None
+
+
+def router(
+    x: torch.Tensor,
+    w_router: torch.Tensor,
+    top_k: int,
+    score_func: str = "softmax",
+    route_norm: bool = False,
+    route_scale: float = 1.0,
+    expert_bias: torch.Tensor | None = None,
+    norm_eps: float = 1e-20,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """UPSTREAM TokenChoiceTopKRouter forward: (top_scores fp32 [T, K],
+    selected_experts_indices int64 [T, K]).  Differentiable in x and w_router
+    when either requires grad (RouterFn), else the plain fused kernel."""
+    if torch.is_grad_enabled() and (x.requires_grad or w_router.requires_grad):
+        return RouterFn.apply(x, w_router, top_k, score_func, route_norm, route_scale, expert_bias, norm_eps)
+    return ops.router_fused(x.reshape(-1, x.shape[-1]).to(_BF16), _bf16(w_router), top_k, score_func, route_norm,
+                            route_scale, expert_bias, norm_eps)
+
+
 class DispatchFn(torch.autograd.Function):
     """routed = gather of token rows in stable expert order (+ score before experts)."""
 

@@ -173,6 +173,48 @@ def router_fused(
     return scores, idx
 
 
+def router_backward(
+    grad_top_scores: torch.Tensor,
+    top_indices: torch.Tensor,
+    logits: torch.Tensor,
+    x: torch.Tensor,
+    w_router: torch.Tensor,
+    score_func: str = "softmax",
+    route_norm: bool = False,
+    route_scale: float = 1.0,
+    norm_eps: float = 1e-20,
+    need_dx: bool = True,
+    need_dw: bool = True,
+    dw_dtype: torch.dtype = torch.float32,
+) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+    """Backward of the router forward (ttamd_router_backward): from
+    d(top_scores) [T, K], the picks and the forward's bf16 logits [T, E] to
+    dx bf16 [T, D] and dW_r [E, D] (fp32 or bf16)."""
+    dev = _gpu("grad_top_scores", grad_top_scores)
+    x = _want("x", x.reshape(-1, x.shape[-1]), _BF16)
+    w_router = _want("w_router", w_router, _BF16)
+    logits = _want("logits", logits, _BF16)
+    T, D = x.shape
+    E = w_router.shape[0]
+    K = top_indices.shape[-1]
+    g = grad_top_scores.reshape(T, K).float().contiguous()
+    idx = top_indices.reshape(T, K).to(torch.int64).contiguous()
+    if tuple(logits.shape) != (T, E):
+        raise ValueError(f"logits must be [{T}, {E}], got {tuple(logits.shape)}")
+    if dw_dtype not in (torch.float32, _BF16):
+        raise TypeError("dw_dtype must be float32 or bfloat16")
+    funcs = {"softmax": 0, "sigmoid": 1}
+    dx = torch.empty(T, D, dtype=_BF16, device=dev) if need_dx else None
+    dw = torch.empty(E, D, dtype=dw_dtype, device=dev) if need_dw else None
+    ws = _ws(_lib.load().ttamd_router_backward_workspace_bytes(T, E, D), dev)
+    _lib.call(
+        "ttamd_router_backward", _p(g), _p(idx), _p(logits), _p(x), _p(w_router), T, E, D, K, funcs[score_func],
+        int(bool(route_norm)), float(norm_eps), float(route_scale), _p(dx), _p(dw), int(dw_dtype == torch.float32),
+        _p(ws), ws.numel(), _stream(dev),
+    )
+    return dx, dw
+
+
 def router_route(
     x: torch.Tensor,
     w_router: torch.Tensor,
@@ -193,6 +235,11 @@ def router_route(
     fp32 [T, K], selected_experts_indices int64 [T, K], RouteResult with
     sorted_scores = top_scores.view(-1)[sorted_indices])."""
     dev = _gpu("x", x)
+    if torch.is_grad_enabled() and (x.requires_grad or w_router.requires_grad):
+        raise RuntimeError(
+            "router_route is the inference path (its scores carry no autograd); for training use "
+            "functional.router (differentiable) followed by route"
+        )
     x = _want("x", x.reshape(-1, x.shape[-1]), _BF16)
     w_router = _want("w_router", w_router, _BF16)
     T, D = x.shape
