@@ -1,8 +1,12 @@
-"""Autograd functions of the MoE expert path (HIP kernels forward and backward).
+"""Autograd-carrying functions of the MoE expert path (HIP kernels forward
+and backward), built on the registered ``ttamd::*`` custom ops of
+``library.py`` so that torch.compile / AOTAutograd trace them as opaque
+nodes with their registered backward.
 
 The split follows the reference's module boundaries so each piece can be used
 on its own:
 
+  router    (UPSTREAM TokenChoiceTopKRouter; closed form qwen3_5/model.py:752-766)
   dispatch  (upstream dispatch, entered from npu_gmm.py:106-108)
       routed[j] = x[s_j // K] (* score[s_j] when score_before_experts)
   experts   (_run_experts_grouped_mm, npu_gmm.py:21-40)
@@ -12,57 +16,38 @@ on its own:
 
 plus the reference's own NPUMoeTokenUnpermute (npu_permute.py:15-53).
 `moe_experts_forward` chains them; without autograd it takes the fused
-route: the score multiply and the un-permute run in the w2 GEMM epilogue.
+inference op (one C-ABI call for the whole expert stage).
 """
 from __future__ import annotations
 
 import torch
 
+from . import library  # noqa: F401  (registers the ttamd::* ops)
 from . import ops
 
 _BF16 = torch.bfloat16
+_T = torch.ops.ttamd
 
 
 def _bf16(w: torch.Tensor) -> torch.Tensor:
     return w if w.dtype == _BF16 else w.to(_BF16)
 
 
-class RouterFn(torch.autograd.Function):
-    """Router forward (gate Linear in bf16 + fp32 softmax / sigmoid + top-k +
-    renorm, UPSTREAM TokenChoiceTopKRouter; closed form
-    torchtitanturbo/models/qwen3_5/model.py:752-766) with its backward on the
-    HIP kernels: d(top_scores) -> d(logits) -> dx, dW_r.  The expert ids
-    carry no gradient."""
+def _needs_grad(*tensors) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors)
+
+
+class RouterFn:
+    """Router forward with its backward (ttamd::router): (top_scores fp32
+    [T, K], selected_experts_indices int64 [T, K]); the expert ids carry no
+    gradient.  x [..., D] and w_router [E, D] in any float dtype (cast to
+    bf16 inside the graph, so their gradients come back in their dtype)."""
 
     @staticmethod
-    def forward(ctx, x, w_router, top_k, score_func, route_norm, route_scale, expert_bias, norm_eps):
-        shape = x.shape
-        xb = x.reshape(-1, shape[-1]).to(_BF16).contiguous()
-        wb = _bf16(w_router).contiguous()
-        scores, idx, logits = ops.router_fused(xb, wb, top_k, score_func, route_norm, route_scale, expert_bias,
-                                               norm_eps, return_logits=True)
-        ctx.save_for_backward(xb, wb, idx, logits)
-        ctx.cfg = (score_func, route_norm, route_scale, norm_eps)
-        ctx.x_shape, ctx.x_dtype, ctx.w_dtype = shape, x.dtype, w_router.dtype
-        ctx.mark_non_differentiable(idx)
+    def apply(x, w_router, top_k, score_func, route_norm, route_scale, expert_bias, norm_eps):
+        xb = x.reshape(-1, x.shape[-1]).to(_BF16).contiguous()
+        scores, idx, _ = _T.router(xb, w_router, top_k, score_func, route_norm, route_scale, expert_bias, norm_eps)
         return scores, idx
-
-    @staticmethod
-    def backward(ctx, g_scores, _g_idx):
-        xb, wb, idx, logits = ctx.saved_tensors
-        func, norm, scale, eps = ctx.cfg
-        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        if g_scores is None or not (need_dx or need_dw):
-            return (None,) * 8
-        dx, dw = ops.router_backward(
-            g_scores, idx, logits, xb, wb, func, norm, scale, eps, need_dx, need_dw,
-            torch.float32 if ctx.w_dtype != _BF16 else _BF16,
-        )
-        if dx is not None:
-            dx = dx.view(ctx.x_shape).to(ctx.x_dtype)
-        if dw is not None:
-            dw = dw.to(ctx.w_dtype)
-        return dx, dw, None, None, None, None, None, None
 
 
 def router(
@@ -76,153 +61,66 @@ def router(
     norm_eps: float = 1e-20,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """UPSTREAM TokenChoiceTopKRouter forward: (top_scores fp32 [T, K],
-    selected_experts_indices int64 [T, K]).  Differentiable in x and w_router
-    when either requires grad (RouterFn), else the plain fused kernel."""
-    if torch.is_grad_enabled() and (x.requires_grad or w_router.requires_grad):
-        return RouterFn.apply(x, w_router, top_k, score_func, route_norm, route_scale, expert_bias, norm_eps)
-    return ops.router_fused(x.reshape(-1, x.shape[-1]).to(_BF16), _bf16(w_router), top_k, score_func, route_norm,
-                            route_scale, expert_bias, norm_eps)
+    selected_experts_indices int64 [T, K]).  Differentiable in x and
+    w_router (ttamd::router's registered backward)."""
+    return RouterFn.apply(x, w_router, top_k, score_func, route_norm, route_scale, expert_bias, norm_eps)
 
 
-class DispatchFn(torch.autograd.Function):
+class DispatchFn:
     """routed = gather of token rows in stable expert order (+ score before experts)."""
 
     @staticmethod
-    def forward(ctx, x, scores_flat, sorted_indices, inverse, sorted_scores, top_k, score_before):
-        ctx.top_k = top_k
-        ctx.score_before = score_before
-        if top_k == 1:
-            routed = ops.gather_rows(x, sorted_indices, 1, sorted_scores if score_before else None)
-        else:
-            routed = ops.dispatch_rows(x, inverse, top_k, scores_flat if score_before else None)
-        ctx.save_for_backward(x, scores_flat, sorted_indices, inverse)
-        return routed
+    def apply(x, scores_flat, sorted_indices, inverse, sorted_scores, top_k, score_before):
+        return _T.dispatch(x, scores_flat, sorted_indices, inverse, sorted_scores, top_k, score_before)
+
+
+class ExpertsFn:
+    """y = (swiglu(clamp(x @ w13[e]^T))) @ w2[e]^T over ragged expert groups;
+    the pre-activation and SwiGLU output are kept only when a backward can
+    follow."""
 
     @staticmethod
-    def backward(ctx, d_routed):
-        x, scores_flat, sorted_indices, inverse = ctx.saved_tensors
-        d_routed = d_routed.to(_BF16).contiguous()
-        dx = dscores = None
-        probs = scores_flat if ctx.score_before else None
-        if ctx.needs_input_grad[0]:
-            dx = ops.combine(d_routed, inverse, probs, ctx.top_k)
-        if ctx.score_before and ctx.needs_input_grad[1]:
-            # d score[s] = <d_routed[pos(s)], x[s // K]>
-            dscores = ops.rowdot_scatter(d_routed, x, sorted_indices, ctx.top_k)
-        return dx, dscores, None, None, None, None, None
-
-
-class ExpertsFn(torch.autograd.Function):
-    """y = (swiglu(clamp(x @ w13[e]^T))) @ w2[e]^T over ragged expert groups."""
-
-    @staticmethod
-    def forward(ctx, routed, w13, w2, offs, swiglu_limit):
-        w13b, w2b = _bf16(w13), _bf16(w2)
-        # autograd runs forward() with grad mode off; needs_input_grad says
-        # whether a backward can follow, i.e. whether h must be kept.
-        need = any(ctx.needs_input_grad[:3])
-        a, h = ops.grouped_mm_swiglu(routed, w13b, offs, swiglu_limit, save_h=need)
-        y = ops.grouped_mm_unpermute(a, w2b, offs)
-        ctx.swiglu_limit = swiglu_limit
-        ctx.w_dtypes = (w13.dtype, w2.dtype)
-        ctx.num_experts = w13.shape[0]
-        if need:
-            ctx.save_for_backward(routed, h, a, w13b, w2b, offs)
+    def apply(routed, w13, w2, offs, swiglu_limit):
+        keep = _needs_grad(routed, w13, w2)
+        y, _, _ = _T.experts(routed, w13, w2, offs, swiglu_limit, keep)
         return y
 
-    @staticmethod
-    def backward(ctx, dy):
-        routed, h, a, w13b, w2b, offs = ctx.saved_tensors
-        dy = dy.to(_BF16).contiguous()
-        E = ctx.num_experts
-        dh, _ = ops.grouped_mm_dgrad_swiglu(dy, w2b, h, offs, ctx.swiglu_limit)
-        d_routed = dw13 = dw2 = None
-        if ctx.needs_input_grad[2]:
-            dw2 = ops.grouped_mm_wgrad(dy, a, offs, E, torch.float32 if ctx.w_dtypes[1] != _BF16 else _BF16)
-            dw2 = dw2.to(ctx.w_dtypes[1])
-        if ctx.needs_input_grad[1]:
-            dw13 = ops.grouped_mm_wgrad(dh, routed, offs, E, torch.float32 if ctx.w_dtypes[0] != _BF16 else _BF16)
-            dw13 = dw13.to(ctx.w_dtypes[0])
-        if ctx.needs_input_grad[0]:
-            d_routed = ops.grouped_mm_dgrad(dh, w13b, offs)
-        return d_routed, dw13, dw2, None, None
 
-
-class CombineFn(torch.autograd.Function):
+class CombineFn:
     """out[t] = sum_k w(t,k) * y[pos(t,k)], w = score if score after experts else 1."""
 
     @staticmethod
-    def forward(ctx, y, scores_flat, sorted_indices, inverse, top_k, score_after):
-        ctx.top_k = top_k
-        ctx.score_after = score_after
-        probs = scores_flat if score_after else None
-        out = ops.combine(y, inverse, probs, top_k)
-        ctx.save_for_backward(y, scores_flat, sorted_indices)
-        return out
-
-    @staticmethod
-    def backward(ctx, dout):
-        y, scores_flat, sorted_indices = ctx.saved_tensors
-        dout = dout.to(_BF16).contiguous()
-        need_ds = ctx.score_after and ctx.needs_input_grad[1]
-        dy, dscores = ops.token_unpermute_grad(
-            dout, sorted_indices, scores_flat if ctx.score_after else None, y if need_ds else None,
-            ctx.top_k, need_probs_grad=need_ds,
-        )
-        return dy, dscores, None, None, None, None
+    def apply(y, scores_flat, sorted_indices, inverse, top_k, score_after):
+        return _T.combine(y, scores_flat, sorted_indices, inverse, top_k, score_after)
 
 
-class HIPMoeTokenUnpermute(torch.autograd.Function):
+class HIPMoeTokenUnpermute:
     """Functional unpermute with backward; same contract as the reference's
     NPUMoeTokenUnpermute (torchtitanturbo/models/common/npu_permute.py:15-53):
     probs=None, top_k=1, empty input passes through.  With one choice per
     row and no probs the unpermute is a pure row scatter,
     out[sorted_indices[j]] = permuted_tokens[j], and its backward the
-    matching gather, so both move rows bit for bit in the input's dtype."""
+    matching gather (ttamd::token_unpermute), so both move rows bit for bit
+    in the input's dtype."""
 
     @staticmethod
-    def forward(ctx, permuted_tokens, sorted_indices, restore_shape):
+    def apply(permuted_tokens, sorted_indices, restore_shape):
         if not permuted_tokens.numel():
             return permuted_tokens
         rows = permuted_tokens.reshape(-1, permuted_tokens.shape[-1])
-        out = ops.scatter_rows_exact(rows, sorted_indices.to(torch.int32))
-        ctx.restore_shape = restore_shape
-        ctx.save_for_backward(sorted_indices)
-        return out.view(restore_shape)
-
-    @staticmethod
-    def backward(ctx, unpermuted_tokens_grad):
-        if not unpermuted_tokens_grad.numel():
-            return unpermuted_tokens_grad, None, None
-        if ctx.needs_input_grad[0]:
-            (sorted_indices,) = ctx.saved_tensors
-            g = unpermuted_tokens_grad.reshape(-1, unpermuted_tokens_grad.shape[-1])
-            act_grad = ops.gather_rows_exact(g, sorted_indices.to(torch.int32))
-            return act_grad, None, None
-        return None, None, None
+        return _T.token_unpermute(rows, sorted_indices).view(restore_shape)
 
 
-class TokenPermuteFn(torch.autograd.Function):
+class TokenPermuteFn:
     """permuted[j] = rows[sorted_indices[j]], sorted_indices the stable order of
     the row labels (torch_npu.npu_moe_token_permute with one label per row,
     npu_permute.py:74-76).  Rows move bit for bit in their own dtype; the
     backward scatters the gradient rows back, grad_rows[sorted_indices[j]] =
-    grad_permuted[j] (npu_moe_token_permute's autograd)."""
+    grad_permuted[j] (ttamd::token_permute)."""
 
     @staticmethod
-    def forward(ctx, rows, labels, num_labels):
-        r = ops.route(labels, num_labels)
-        permuted = ops.gather_rows_exact(rows, r.sorted_indices)
-        ctx.save_for_backward(r.sorted_indices)
-        ctx.mark_non_differentiable(r.sorted_indices)
-        return permuted, r.sorted_indices
-
-    @staticmethod
-    def backward(ctx, grad_permuted, _grad_idx):
-        (sorted_indices,) = ctx.saved_tensors
-        if not ctx.needs_input_grad[0]:
-            return None, None, None
-        return ops.scatter_rows_exact(grad_permuted.contiguous(), sorted_indices), None, None
+    def apply(rows, labels, num_labels):
+        return _T.token_permute(rows, labels, num_labels)
 
 
 def run_experts_grouped_mm(
@@ -251,17 +149,13 @@ def shared_expert_combine(
     (torchtitanturbo/models/qwen3_5/model.py:796-809; UPSTREAM Llama4 adds the
     ungated shared expert).  x [T, D]; w13_shared [2H, D]; w2_shared [D, H].
 
-    Without autograd this is one fused pass (ttamd_shared_expert_add: the
+    Without autograd this is one fused pass (ttamd::shared_expert_add: the
     shared w2 GEMM adds into the routed output in its epilogue).  With
-    autograd it runs the shared FFN as a one-expert ExpertsFn and composes
-    the gate and the sum in torch, so every input gets its gradient."""
-    needs_grad = torch.is_grad_enabled() and any(
-        t is not None and t.requires_grad for t in (routed_out, x, w13_shared, w2_shared, gate_logits))
-    if not needs_grad:
-        out = routed_out.to(_BF16).contiguous().clone()
-        ops.shared_expert_add(out, x.to(_BF16), w13_shared, w2_shared,
-                              None if gate_logits is None else gate_logits.float(), swiglu_limit)
-        return out
+    autograd it runs the shared FFN as a one-expert ttamd::experts and
+    composes the gate and the sum in torch, so every input gets its
+    gradient."""
+    if not _needs_grad(routed_out, x, w13_shared, w2_shared, gate_logits):
+        return _T.shared_expert_add(routed_out, x, w13_shared, w2_shared, gate_logits, swiglu_limit)
     T = x.shape[0]
     all_rows = torch.full((1,), T, dtype=torch.int32, device=x.device)
     y = ExpertsFn.apply(x.to(_BF16).contiguous(), w13_shared.unsqueeze(0), w2_shared.unsqueeze(0), all_rows,
@@ -285,7 +179,7 @@ def moe_experts_forward(
     """dispatch -> experts -> combine for one GPU; x [T, D], scores/indices [T, K] -> [T, D].
 
     With autograd off (or nothing requiring grad) the expert stage is one
-    C-ABI call (ops.experts_forward: both grouped GEMMs on one tile table,
+    op (ttamd::moe_experts_forward: both grouped GEMMs on one tile table,
     the score multiply and the un-permute in the w2 GEMM epilogue).
     ``stage_events``, when given (inference path only), runs the same kernels
     one op at a time and receives a (start, end) pair of torch.cuda.Event
@@ -294,9 +188,7 @@ def moe_experts_forward(
     """
     T, D = x.shape
     K = top_scores.shape[-1]
-    training = torch.is_grad_enabled() and any(
-        t.requires_grad for t in (x, top_scores, w13, w2)
-    )
+    training = _needs_grad(x, top_scores, w13, w2)
     ev = stage_events if (stage_events is not None and not training) else None
 
     def mark(name: str, end: bool) -> None:
@@ -306,14 +198,18 @@ def moe_experts_forward(
 
     scores_flat = top_scores.reshape(-1).float()
     mark("route", False)
-    r = ops.route(selected_experts_indices, num_experts, scores_flat)
+    counts, offsets, sorted_idx, inverse, sorted_scores = _T.route(
+        selected_experts_indices.reshape(-1), num_experts, scores_flat.detach())
     mark("route", True)
-    offs = r.offs
+    offs = offsets[1:]
     xb = x.to(_BF16).contiguous()
     if not training and ev is None and D % 128 == 0:
-        out = ops.experts_forward(xb, r, _bf16(w13), _bf16(w2), K, score_before_experts, swiglu_limit)
+        out = _T.moe_experts_forward(xb, sorted_idx, offsets, sorted_scores, _bf16(w13), _bf16(w2), K,
+                                     score_before_experts, swiglu_limit)
         return out.to(x.dtype)
     if not training:
+        # op-at-a-time over the same kernels (stage timing; D < 128)
+        r = ops.RouteResult(counts, offsets, sorted_idx, inverse, sorted_scores)
         w13b, w2b = _bf16(w13), _bf16(w2)
         if score_before_experts or D < 128:
             mark("permute", False)
@@ -340,11 +236,9 @@ def moe_experts_forward(
             out = ops.sum_topk(ybuf, K)
             mark("sum_topk", True)
         return out.to(x.dtype)
-    routed = DispatchFn.apply(
-        xb, scores_flat, r.sorted_indices, r.inverse, r.sorted_scores, K, score_before_experts
-    )
+    routed = DispatchFn.apply(xb, scores_flat, sorted_idx, inverse, sorted_scores, K, score_before_experts)
     y = ExpertsFn.apply(routed, w13, w2, offs, swiglu_limit)
-    out = CombineFn.apply(y, scores_flat, r.sorted_indices, r.inverse, K, not score_before_experts)
+    out = CombineFn.apply(y, scores_flat, sorted_idx, inverse, K, not score_before_experts)
     return out.to(x.dtype)
 
 
