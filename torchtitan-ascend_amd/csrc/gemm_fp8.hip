@@ -141,9 +141,11 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
       // block), lane 1 + q the up block of weight quarter q (with H % 128 ==
       // 64 the tile's up rows straddle two blocks; a quarter's 32 do not).
       const int64_t kb_n = a.kred / TKB;
+      // (32-bit: H < 2^20, so hidden + 128 pt + 96 fits; a 64-bit lane value
+      // here was kept live through the k loop and spilled)
       int blk;
       if constexpr (EPI == EPI_SWIGLU)
-        blk = (l == 0) ? pt : (int)((a.hidden + (int64_t)pt * 128 + 32 * min(l - 1, 3)) / 128);
+        blk = (l == 0) ? pt : ((int)a.hidden + pt * 128 + 32 * min(l - 1, 3)) >> 7;
       else
         blk = 2 * pt + (l & 1);
       blk = min(blk, a.n_p / 128 - 1);
@@ -229,11 +231,14 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
       if (s + 1 < total) issue(s + 1);
       const char* st = smem + (s % NSTAGE) * STAGE_BYTES;
       i32x8_t fa[NPB16];
+      // A block's weight scale is one value for the whole wave (every lane
+      // reads the same LDS word): kept in SGPRs, it frees VGPRs for the
+      // accumulators and fragments.
       float swv[NPB16];
 #pragma unroll
       for (int pb = 0; pb < NPB16; ++pb) {
         fa[pb] = frag16(st, arow[pb]);
-        swv[pb] = *(const float*)(st + SW_OFF + sw_lane(pb) * 4);
+        swv[pb] = __int_as_float(__builtin_amdgcn_readfirstlane(*(const int*)(st + SW_OFF + sw_lane(pb) * 4)));
       }
       i32x8_t fb[NBS];
       float sxv[NBS];
@@ -271,9 +276,13 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
     }
 
     // ---- epilogue: acc[pb][jb][i] is (token row 128wq + 16jb + lane % 16,
-    //      weight row arow[pb] + 4 (lane / 16) + i).
-    int er16 = r16;
-    asm volatile("" : "+v"(er16));
+    //      weight row arow[pb] + 4 (lane / 16) + i).  The lane's row and
+    //      column group are re-derived here from an opaque copy of the lane
+    //      id, so that nothing epilogue-only stays live through the k loop.
+    int el = l;
+    asm volatile("" : "+v"(el));
+    const int er16 = el & 15;
+    const int eg4 = el >> 4;
 #pragma unroll
     for (int jb = 0; jb < NJ16; ++jb) {
       const int gq = row0 + 128 * wq + 16 * jb + er16;
@@ -285,7 +294,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
         if (pt * 128 + 32 * wp >= a.hidden) continue;
 #pragma unroll
         for (int pb = 0; pb < 2; ++pb) {
-          const int col = pt * 128 + arow[pb] + 4 * g4;
+          const int col = pt * 128 + arow[pb] + 4 * eg4;
           float av[4], gv[4], uv[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -320,7 +329,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
         bf16_t* orow = a.out + (int64_t)orow_idx * a.ldo;
 #pragma unroll
         for (int pb = 0; pb < NPB16; ++pb) {
-          const int col = pt * TP + arow[pb] + 4 * g4;
+          const int col = pt * TP + arow[pb] + 4 * eg4;
           const floatx4_t& v = acc[pb][jb];
           const uint2 val = make_uint2(pack_bf16x2(v[0] * scl, v[1] * scl), pack_bf16x2(v[2] * scl, v[3] * scl));
           if (row_ok) *(uint2*)(orow + col) = val;
