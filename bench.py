@@ -58,6 +58,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="capture the inference step once as a HIP graph and time its replays (one launch per "
+                         "step instead of the host's per-call cost); the roofline probe then runs in extra eager "
+                         "steps after the timed ones")
     ap.add_argument("--staged", action="store_true",
                     help="time the op-at-a-time path (router, route, then each GEMM and the sum as its own call) "
                          "instead of the two fused C-ABI calls")
@@ -229,8 +233,21 @@ def main():
     # kernel's stream immediately around that one kernel, in every timed
     # step.  (Event records between kernels cost GPU time, ~3 us each; the
     # per-stage breakdown is therefore taken from separate steps below.)
+    graph = None
+    if args.graph:
+        if cfg["backward"] or fp8 or args.staged:
+            print(json.dumps({"error": "--graph covers the bf16 inference step (two C-ABI calls) only"}))
+            sys.exit(2)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        for _ in range(max(args.warmup, 3)):
+            graph.replay()
+        torch.cuda.synchronize()
+        log("captured the step as one HIP graph")
+    n_probe = args.steps if graph is None else min(args.steps, 50)
     probes = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(args.steps)]
+              for _ in range(n_probe)]
     for pair in probes:
         for e in pair:
             e.record()  # creates the HIP events outside the timed region
@@ -238,10 +255,19 @@ def main():
     torch.cuda.synchronize()
     start.record()
     for i in range(args.steps):
-        ops.probe_next_gemm(*probes[i])
-        step()
+        if graph is not None:
+            graph.replay()
+        else:
+            ops.probe_next_gemm(*probes[i])
+            step()
     end.record()
     torch.cuda.synchronize()
+    if graph is not None:
+        # the probe needs the host launch path: extra eager steps, untimed
+        for pair in probes:
+            ops.probe_next_gemm(*pair)
+            step()
+        torch.cuda.synchronize()
     ops.probe_next_gemm(None, None)
     ms = start.elapsed_time(end) / args.steps
     kernel_us = sum(p[0].elapsed_time(p[1]) for p in probes) * 1000.0 / len(probes)
@@ -300,6 +326,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "clock_settle": {"ms": args.settle_ms, "steps": settle_steps},
+        "hip_graph": graph is not None,
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
