@@ -25,6 +25,8 @@
 //     score + top-k with 16 lanes per token (4 tokens per wave).
 // The split count S is chosen so that the first kernel has about one
 // workgroup per CU.
+#include <type_traits>
+
 #include "common.h"
 #include "dma_asm.h"
 #include "gemm_common.h"
@@ -172,44 +174,71 @@ struct RouterTopkArgs {
   int nchunks, chunk;
 };
 
-// (selection value desc, expert id asc) winner, with its unbiased score.
+// Order-preserving unsigned key of a selection value: a larger value has a
+// larger key.  The selection is a strict '>' scan that starts from -inf, so
+// -inf and NaN are never picked: both map to 0, the key of a slot already
+// picked.  -0 becomes +0 first (they compare equal as floats).
+__device__ __forceinline__ uint32_t sel_key(float v) {
+  const uint32_t b = __float_as_uint(v + 0.f);
+  const uint32_t k = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+  return v > -INFINITY ? k : 0u;
+}
+
 template <int CTRL>
-__device__ __forceinline__ void argmax_step(float& bv, int& bi, float& bs) {
-  const float ov = dpp_f<CTRL>(bv);
-  const int oi = dpp_i<CTRL>(bi);
-  const float os = dpp_f<CTRL>(bs);
-  if (ov > bv || (ov == bv && oi < bi)) {
-    bv = ov;
-    bi = oi;
-    bs = os;
-  }
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)dpp_i<CTRL>((int)v);
+}
+
+// Unsigned max / min over the 16 lanes of a DPP row (every lane gets it).
+__device__ __forceinline__ uint32_t row16_umax(uint32_t v) {
+  v = max(v, dpp_u<kDppXor1>(v));
+  v = max(v, dpp_u<kDppXor2>(v));
+  v = max(v, dpp_u<kDppHalfMirror>(v));
+  return max(v, dpp_u<kDppMirror>(v));
+}
+__device__ __forceinline__ uint32_t row16_umin(uint32_t v) {
+  v = min(v, dpp_u<kDppXor1>(v));
+  v = min(v, dpp_u<kDppXor2>(v));
+  v = min(v, dpp_u<kDppHalfMirror>(v));
+  return min(v, dpp_u<kDppMirror>(v));
 }
 
 // 16 lanes per token, 4 tokens per wave, 16 tokens per workgroup.  Lane i
 // holds experts in runs of G = min(PL, 4) consecutive ids,
 // e(m) = G i + m % G + 16 G (m / G), so each run of partials is one 4G-byte
-// load (the 16 lanes of a token read 64 G contiguous bytes per run).
-template <int PL>
+// load (the 16 lanes of a token read 64 G contiguous bytes per run).  FULL:
+// E == 16 PL, every slot holds an expert.
+//
+// Selection: each of the K rounds takes the largest key of the row (DPP
+// max), then the lowest expert id holding it (DPP min) -- the (value desc,
+// id asc) order of a stable top-k -- and clears that slot.  The picked
+// scores reach their output lanes through LDS and are summed in pick order
+// for the renormalisation.
+template <int PL, bool FULL>
 __global__ __launch_bounds__(256) void router_topk_partials_kernel(const RouterTopkArgs a) {
   constexpr int G = PL < 4 ? PL : 4;
+  __shared__ __attribute__((aligned(16))) float lsc[16][16 * PL];  // scores by expert id
+  __shared__ float lpick[16][16];                                  // picked scores, pick order
   const int l = threadIdx.x & 63;
   const int gi = l & 15;
-  const int t = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int tl = threadIdx.x >> 4;
+  const int t = blockIdx.x * 16 + tl;
   const bool valid = t < a.T;
   const int tt = valid ? t : a.T - 1;
+  const int E = FULL ? 16 * PL : a.E;
   auto eid = [&](int m) { return G * gi + m % G + 16 * G * (m / G); };
-  float sc[PL], sel[PL];
+  auto live = [&](int m) { return FULL || eid(m) < E; };
   // every partial first (one batch of independent loads), then the sums in
   // split order
   float pv[kRouterMaxSplits][PL];
-  const bool vec = (a.E % G) == 0;  // runs never straddle E and stay aligned
+  const bool vec = FULL || (E % G) == 0;  // runs never straddle E and stay aligned
 #pragma unroll
   for (int s = 0; s < kRouterMaxSplits; ++s)
 #pragma unroll
     for (int m0 = 0; m0 < PL; m0 += G) {
       const int e0 = eid(m0);
-      const float* src = a.part + ((int64_t)s * a.T + tt) * a.E + e0;
-      if (s < a.S && vec && e0 < a.E) {
+      const float* src = a.part + ((int64_t)s * a.T + tt) * E + e0;
+      if (s < a.S && vec && (FULL || e0 < E)) {
         if constexpr (G == 4) {
           const float4 v = *(const float4*)src;
           pv[s][m0] = v.x; pv[s][m0 + 1] = v.y; pv[s][m0 + 2] = v.z; pv[s][m0 + 3] = v.w;
@@ -221,32 +250,46 @@ __global__ __launch_bounds__(256) void router_topk_partials_kernel(const RouterT
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < G; ++i) pv[s][m0 + i] = (s < a.S && e0 + i < a.E) ? src[i] : 0.f;
+        for (int i = 0; i < G; ++i) pv[s][m0 + i] = (s < a.S && e0 + i < E) ? src[i] : 0.f;
       }
     }
+  float sc[PL];
   float mx = -INFINITY;
 #pragma unroll
   for (int m = 0; m < PL; ++m) {
-    const int e = eid(m);
     float z = -INFINITY;
-    if (e < a.E) {
+    if (live(m)) {
       z = pv[0][m];
 #pragma unroll
       for (int s = 1; s < kRouterMaxSplits; ++s)
         if (s < a.S) z += pv[s][m];
       z = round_bf16(z);
-      if (a.logits && valid) a.logits[(int64_t)t * a.E + e] = (bf16_t)f32_to_bf16(z);
     }
     sc[m] = z;
     mx = fmaxf(mx, z);
+  }
+  if (a.logits && valid) {
+    bf16_t* lrow = a.logits + (int64_t)t * E;
+#pragma unroll
+    for (int m0 = 0; m0 < PL; m0 += G) {
+      const int e0 = eid(m0);
+      if constexpr (FULL && G == 4) {
+        *(u32x2_t*)(lrow + e0) = u32x2_t{pack_bf16x2(sc[m0], sc[m0 + 1]), pack_bf16x2(sc[m0 + 2], sc[m0 + 3])};
+      } else if constexpr (FULL && G == 2) {
+        *(uint32_t*)(lrow + e0) = pack_bf16x2(sc[m0], sc[m0 + 1]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < G; ++i)
+          if (e0 + i < E) lrow[e0 + i] = (bf16_t)f32_to_bf16(sc[m0 + i]);
+      }
+    }
   }
   if (a.score_func == 0) {
     mx = row16_max(mx);
     float sum = 0.f;
 #pragma unroll
     for (int m = 0; m < PL; ++m) {
-      const int e = eid(m);
-      sc[m] = (e < a.E) ? expf(sc[m] - mx) : 0.f;
+      sc[m] = live(m) ? expf(sc[m] - mx) : 0.f;
       sum += sc[m];
     }
     sum = row16_sum(sum);
@@ -256,62 +299,75 @@ __global__ __launch_bounds__(256) void router_topk_partials_kernel(const RouterT
 #pragma unroll
     for (int m = 0; m < PL; ++m) sc[m] = 1.f / (1.f + expf(-sc[m]));
   }
+  uint32_t key[PL];
 #pragma unroll
-  for (int m = 0; m < PL; ++m) {
-    const int e = eid(m);
-    sel[m] = (e < a.E) ? (a.bias ? sc[m] + a.bias[e] : sc[m]) : -INFINITY;
-  }
-  float picked = 0.f, my_v = 0.f;
+  for (int m = 0; m < PL; ++m) key[m] = live(m) ? sel_key(a.bias ? sc[m] + a.bias[eid(m)] : sc[m]) : 0u;
   int my_i = 0;
+  bool my_deg = false;
   for (int k = 0; k < a.K; ++k) {
-    float bv = -INFINITY, bs = 0.f;
-    int bi = 0x7fffffff;
+    uint32_t km = key[0];
 #pragma unroll
-    for (int m = 0; m < PL; ++m) {
-      const int e = eid(m);
-      if (e < a.E && (sel[m] > bv || (sel[m] == bv && e < bi))) {
-        bv = sel[m];
-        bi = e;
-        bs = sc[m];
-      }
-    }
-    argmax_step<kDppXor1>(bv, bi, bs);
-    argmax_step<kDppXor2>(bv, bi, bs);
-    argmax_step<kDppHalfMirror>(bv, bi, bs);
-    argmax_step<kDppMirror>(bv, bi, bs);
-    bi = min(max(bi, 0), a.E - 1);  // K <= E keeps a valid pick; stay in range regardless
+    for (int m = 1; m < PL; ++m) km = max(km, key[m]);
+    km = row16_umax(km);
+    uint32_t cand = 0xffffffffu;
 #pragma unroll
-    for (int m = 0; m < PL; ++m)
-      if (eid(m) == bi) sel[m] = -INFINITY;
-    picked += bs;
+    for (int m = PL - 1; m >= 0; --m) cand = (key[m] == km) ? (uint32_t)eid(m) : cand;
+    cand = row16_umin(cand);
+    // km == 0: nothing pickable is left (K > the finite scores): expert E - 1
+    // with score 0
+    const bool deg = km == 0u;
+    const int win = deg ? E - 1 : (int)cand;
+#pragma unroll
+    for (int m = 0; m < PL; ++m) key[m] = (eid(m) == win) ? 0u : key[m];
     if (gi == k) {
-      my_v = bs;
-      my_i = bi;
+      my_i = win;
+      my_deg = deg;
     }
   }
-  if (gi < a.K && valid) {
+  const bool out = gi < a.K;
+  if (a.hist) {
+    // The workgroup's 16 K flat slots (K <= 16) span at most two chunks:
+    // count them in LDS, then one atomic per nonzero (expert, chunk),
+    // issued before the score exchange so that their round trips overlap it.
+    __shared__ int lh[2 * kRouterMaxE];
+    const int c0 = (int)(((int64_t)blockIdx.x * 16 * a.K) / a.chunk);
+    for (int i = threadIdx.x; i < 2 * E; i += 256) lh[i] = 0;
+    __syncthreads();
+    if (out && valid) {
+      const int c = (int)(((int64_t)t * a.K + gi) / a.chunk) - c0;  // 0 or 1
+      atomicAdd(&lh[min(max(c, 0), 1) * E + my_i], 1);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 2 * E; i += 256) {
+      const int n = lh[i];
+      const int c = c0 + i / E;
+      if (n > 0 && c < a.nchunks) atomicAdd(&a.hist[(int64_t)(i % E) * a.nchunks + c], n);
+    }
+  }
+  // scores of the picks: the owner lanes publish, the output lanes read
+  float* srow = lsc[tl];
+#pragma unroll
+  for (int m0 = 0; m0 < PL; m0 += G) {
+    const int e0 = eid(m0);
+    if constexpr (FULL && G == 4) {
+      *(float4*)(srow + e0) = make_float4(sc[m0], sc[m0 + 1], sc[m0 + 2], sc[m0 + 3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < G; ++i)
+        if (e0 + i < 16 * PL) srow[e0 + i] = sc[m0 + i];
+    }
+  }
+  lds_wait();
+  const float my_v = (out && !my_deg) ? srow[my_i] : 0.f;
+  lpick[tl][gi] = my_v;
+  lds_wait();
+  float picked = 0.f;
+  for (int k = 0; k < a.K; ++k) picked += lpick[tl][k];
+  if (out && valid) {
     float v = my_v;
     if (a.renorm) v = v / (picked + a.eps);
     a.scores[(int64_t)t * a.K + gi] = v * a.route_scale;
     a.idx[(int64_t)t * a.K + gi] = my_i;
-  }
-  if (a.hist) {
-    // The workgroup's 16 K flat slots (K <= 16) span at most two chunks:
-    // count them in LDS, then one atomic per nonzero (expert, chunk).
-    __shared__ int lh[2 * kRouterMaxE];
-    const int c0 = (int)(((int64_t)blockIdx.x * 16 * a.K) / a.chunk);
-    for (int i = threadIdx.x; i < 2 * a.E; i += 256) lh[i] = 0;
-    __syncthreads();
-    if (gi < a.K && valid) {
-      const int c = (int)(((int64_t)t * a.K + gi) / a.chunk) - c0;  // 0 or 1
-      atomicAdd(&lh[min(max(c, 0), 1) * a.E + my_i], 1);
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < 2 * a.E; i += 256) {
-      const int n = lh[i];
-      const int c = c0 + i / a.E;
-      if (n > 0 && c < a.nchunks) atomicAdd(&a.hist[(int64_t)(i % a.E) * a.nchunks + c], n);
-    }
   }
 }
 
@@ -532,10 +588,15 @@ hipError_t launch_router_hist(const void* x, const void* w, const float* bias, i
   k.nchunks = nchunks;
   k.chunk = route_chunk_labels();
   const dim3 grid((T + 15) / 16);
-  if (E <= 32) hipLaunchKernelGGL(router_topk_partials_kernel<2>, grid, dim3(256), 0, stream, k);
-  else if (E <= 64) hipLaunchKernelGGL(router_topk_partials_kernel<4>, grid, dim3(256), 0, stream, k);
-  else if (E <= 128) hipLaunchKernelGGL(router_topk_partials_kernel<8>, grid, dim3(256), 0, stream, k);
-  else hipLaunchKernelGGL(router_topk_partials_kernel<16>, grid, dim3(256), 0, stream, k);
+  auto go = [&](auto pl) {
+    constexpr int PL = decltype(pl)::value;
+    if (E == 16 * PL) hipLaunchKernelGGL((router_topk_partials_kernel<PL, true>), grid, dim3(256), 0, stream, k);
+    else hipLaunchKernelGGL((router_topk_partials_kernel<PL, false>), grid, dim3(256), 0, stream, k);
+  };
+  if (E <= 32) go(std::integral_constant<int, 2>{});
+  else if (E <= 64) go(std::integral_constant<int, 4>{});
+  else if (E <= 128) go(std::integral_constant<int, 8>{});
+  else go(std::integral_constant<int, 16>{});
   return hipGetLastError();
 }
 

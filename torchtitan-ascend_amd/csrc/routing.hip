@@ -148,6 +148,7 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
 // GEMMs' tile table of the expert-sorted rows, each when its pointer is set.
 constexpr int kFusedScanMax = 32768;
 constexpr int kBucketsPerThread = (1024 + 1 + kRouteThreads - 1) / kRouteThreads;  // E <= 1024
+constexpr int kRowPrefetch = 64;  // chunk counts per bucket row loaded up front (FUSED, E < 256)
 
 struct RouteExtras {
   int* counts;                // int32 [E]
@@ -168,26 +169,57 @@ __global__ __launch_bounds__(kRouteThreads) void route_rank_kernel(
   // [kRouteWaves][E + 1] wave counters; FUSED: + chunk bases [E + 1],
   // bucket starts [E + 1] and kRouteWaves + 1 scan ints
   extern __shared__ int sh_cnt[];
+  constexpr int NS = kRoutePerWave / kWave;
   const int E1 = E + 1;
   const int w = threadIdx.x / kWave, l = lane_id();
+  const int wbase = blockIdx.x * kRouteChunk + w * kRoutePerWave;
+  // Every global load of the pass is issued here, before the first LDS
+  // wait, so that their latencies overlap: the wave's labels and scores and
+  // (FUSED, one bucket row per thread) the row's first kRowPrefetch chunk
+  // counts.
+  // (Unconditional loads at clamped indices, M >= 1: a branch per load
+  // would make the compiler wait for each before the next.)
+  IdxT lab[NS];
+  float scv[NS];
+  const bool have_scores = sorted_scores != nullptr;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int gc = min(wbase + s * kWave + l, M - 1);
+    lab[s] = labels[gc];
+    scv[s] = have_scores ? scores[gc] : 0.f;
+  }
+  const int per = (E1 + kRouteThreads - 1) / kRouteThreads;
+  // rows of a multiple of 4 counts are read as 16-byte vectors (the
+  // histogram is 256-byte aligned)
+  const bool row_pref = FUSED && per == 1 && nchunks <= kRowPrefetch && (nchunks & 3) == 0;
+  int4 hv[FUSED ? kRowPrefetch / 4 : 1];
+  if constexpr (FUSED) {
+    const int4* row = (const int4*)(base + (size_t)threadIdx.x * nchunks);
+    const bool have = row_pref && (int)threadIdx.x < E1;
+#pragma unroll
+    for (int c = 0; c < kRowPrefetch / 4; ++c) hv[c] = (have && 4 * c < nchunks) ? row[c] : make_int4(0, 0, 0, 0);
+  }
+  int bucket[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const IdxT v = lab[s];
+    bucket[s] = (wbase + s * kWave + l < M) ? ((v >= 0 && v < (IdxT)E) ? (int)v : E) : 0;
+  }
   for (int i = threadIdx.x; i < kRouteWaves * E1; i += kRouteThreads) sh_cnt[i] = 0;
   __syncthreads();
 
-  const int wbase = blockIdx.x * kRouteChunk + w * kRoutePerWave;
-  int bucket[kRoutePerWave / kWave];
-  uint64_t peers[kRoutePerWave / kWave];
+  uint64_t peers[NS];
 #pragma unroll
-  for (int s = 0; s < kRoutePerWave / kWave; ++s) {
+  for (int s = 0; s < NS; ++s) {
     const int g = wbase + s * kWave + l;
     const bool valid = g < M;
-    const int b = valid ? bucket_of(labels, g, E) : 0;
+    const int b = bucket[s];
     uint64_t mask = ballot64(valid);
     for (int bit = 0; bit < nbits; ++bit) {
       const bool set = (b >> bit) & 1;
       const uint64_t bb = ballot64(set);
       mask &= set ? bb : ~bb;
     }
-    bucket[s] = b;
     peers[s] = mask;
     // One leader per distinct bucket of this step: no two lanes of the wave
     // touch the same counter, and other waves use their own row.
@@ -202,14 +234,25 @@ __global__ __launch_bounds__(kRouteThreads) void route_rank_kernel(
     int* sh_scan = sh_start + E1;
     // thread tid owns the consecutive buckets [tid * per, tid * per + per)
     const int tid = threadIdx.x;
-    const int per = (E1 + kRouteThreads - 1) / kRouteThreads;
     int tot[kBucketsPerThread], pre[kBucketsPerThread];
     int mine = 0;
 #pragma unroll
     for (int i = 0; i < kBucketsPerThread; ++i) {
       const int b = tid * per + i;
       tot[i] = pre[i] = 0;
-      if (i < per && b < E1) {
+      if (row_pref) {
+        if (i == 0) {
+#pragma unroll
+          for (int c = 0; c < kRowPrefetch / 4; ++c) {
+            const int q[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              tot[0] += q[u];
+              if (4 * c + u < (int)blockIdx.x) pre[0] += q[u];
+            }
+          }
+        }
+      } else if (i < per && b < E1) {
         const int* row = base + (size_t)b * nchunks;
         int c = 0;
         for (; c + 8 <= nchunks; c += 8) {
@@ -297,7 +340,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_rank_kernel(
       pos = min(max(pos, 0), M - 1);
       sorted_idx[pos] = g;
       if (inverse) inverse[g] = pos;
-      if (sorted_scores) sorted_scores[pos] = scores[g];
+      if (sorted_scores) sorted_scores[pos] = scv[s];
     }
   }
 }
