@@ -15,7 +15,9 @@ library records on the kernel's stream immediately around it) and
 `cpu_baseline` (the reference op sequence restated in torch, timed on this
 host's CPU cores on a bounded sample of the workload).
 
-Other configs (--config c1|c3|c4|c5) are for development runs.
+Other configs (--config c1|c3|c4|c5) are for development runs; C4 and C5
+also time the expert-parallel regroup (`regroup`: the dispatcher's _permute
+with each local expert's rows arriving from 8 ranks).
 """
 from __future__ import annotations
 
@@ -34,6 +36,7 @@ METRIC = "MoE-layer tokens/s + grouped-GEMM TFLOP/s (% MFMA peak), Qwen3-30B-A3B
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_FP8_TFLOPS = 5000.0  # MI355X dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0
+EP_REGROUP = 8  # C4/C5: DeepSeek-V3's 256 experts over 8 ranks, 32 local
 
 CONFIGS = {
     "c1": dict(name="C1 Llama4-debugmodel MoE FFN forward", T=2048, D=256, H=512, E=8, K=1, router="sigmoid",
@@ -123,6 +126,10 @@ def main():
         lab = rng.permutation(np.repeat(np.arange(E), counts))
         zipf_idx = torch.from_numpy(lab.reshape(T, K)).to(dev)
         zipf_scores = torch.rand(T, K, device=dev)
+        # the expert-parallel receive side of the same shard: each local
+        # expert's rows arrive split over EP_REGROUP ranks (rank-major)
+        counts_group = np.stack([rng.multinomial(int(n), np.full(EP_REGROUP, 1.0 / EP_REGROUP))
+                                 for n in counts], axis=1).reshape(-1)
 
     def router():
         if zipf_idx is not None:
@@ -313,6 +320,14 @@ def main():
         permute_bytes = T * D * 2 + M * D * 2 + 8 * M
         permute_us = stage_us.get("permute") or time_standalone_permute(ops, router, x, E, K, cfg)
     permute_gbs = permute_bytes / (permute_us * 1e-6) / 1e9
+    regroup = None
+    if cfg["router"] == "zipf":
+        regroup_us = time_regroup(ops, x, counts_group, E)
+        regroup_bytes = 2 * M * D * 2 + 8 * M
+        regroup_gbs = regroup_bytes / (regroup_us * 1e-6) / 1e9
+        regroup = {"ep": EP_REGROUP, "us": round(regroup_us, 2), "bytes": regroup_bytes,
+                   "gbs": round(regroup_gbs, 1), "frac_of_hbm": round(regroup_gbs / PEAK_HBM_GBS, 4)}
+        log(f"regroup (ep={EP_REGROUP}): {regroup_us:.1f} us, {regroup_gbs:.0f} GB/s")
     peak = PEAK_FP8_TFLOPS if fp8 else PEAK_BF16_TFLOPS
 
     fwd_flops = 6.0 * M * D * H + (6.0 * T * D * H if cfg.get("shared") else 0.0)
@@ -345,6 +360,7 @@ def main():
         "permute_gbs": round(permute_gbs, 1),
         "permute_frac_of_hbm": round(permute_gbs / PEAK_HBM_GBS, 4),
         "stage_us": {k: round(v, 2) for k, v in stage_us.items()},
+        "regroup": regroup,
         "roofline": {
             "kernel": roofline_kernel_name(cfg, fp8),
             "bound": "mfma",
@@ -392,6 +408,36 @@ def time_standalone_permute(ops, router, x, E, K, cfg, reps=20):
         s0.record()
         for _ in range(reps):
             ops.permute_rows(x, r, K, scale)
+        s1.record()
+        torch.cuda.synchronize()
+    return s0.elapsed_time(s1) * 1000.0 / reps
+
+
+def time_regroup(ops, x, counts_group, E, reps=20):
+    """Average duration (us) of the dispatcher's expert-parallel regroup
+    (HipTokenDispatcher._permute at ep > 1; reference
+    NpuTokenDispatcher._permute, npu_permute.py:63-85): the routed rows, received
+    rank-major as (rank, local expert) groups, labelled by group_labels and
+    moved expert-major by token_permute (stable order + one row gather), on
+    the current stream.  Bytes: read and write M rows plus the indices."""
+    import numpy as np
+    import torch
+
+    cg = torch.from_numpy(counts_group.astype(np.int32)).to(x.device)
+    M = x.shape[0]
+
+    def once():
+        labels = ops.group_labels(cg, E, M)
+        return ops.token_permute(x, labels, E)
+
+    with torch.no_grad():
+        for _ in range(3):
+            once()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s0.record()
+        for _ in range(reps):
+            once()
         s1.record()
         torch.cuda.synchronize()
     return s0.elapsed_time(s1) * 1000.0 / reps

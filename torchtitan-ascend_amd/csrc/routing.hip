@@ -503,55 +503,51 @@ hipError_t launch_route(const void* labels, bool is64, int M, int E,
 }
 
 // ---------------------------------------------------------------------------
-// Row movement.  Rows are moved as 16-byte chunks (8 bf16); a thread handles
-// kUnroll chunks per iteration so several loads are in flight.
+// Row movement.  Rows are moved as 16-byte chunks (8 bf16).
 // ---------------------------------------------------------------------------
 constexpr int kMoveThreads = 256;
-constexpr int kUnroll = 4;
-
-static int move_grid(int64_t total_chunks) {
-  int64_t g = (total_chunks + (int64_t)kMoveThreads * kUnroll - 1) / ((int64_t)kMoveThreads * kUnroll);
-  if (g < 1) g = 1;
-  if (g > 8192) g = 8192;
-  return (int)g;
-}
 
 // out[r] = in[clamp(src[r] / div)] * (scale ? scale[scale_by_src ? src[r] : r] : 1)
-__global__ __launch_bounds__(kMoveThreads) void gather_rows_kernel(
+// One wave per output row (grid-stride over rows): the source row id and
+// scale are read once per row, then the row moves in batches of
+// kGatherUnroll 16-byte chunks per lane, every load of a batch issued before
+// its stores.  Both the read and the write of a row are contiguous.
+constexpr int kGatherUnroll = 8;
+
+__global__ __launch_bounds__(256) void gather_rows_kernel(
     const uint4* __restrict__ in, const int* __restrict__ src,
     const float* __restrict__ scale, int scale_by_src, int n_in, int n_src_max,
     int rows, int cpr, int div, uint4* __restrict__ out) {
-  const int total = rows * cpr;
-  const int stride = gridDim.x * kMoveThreads;
-  for (int base = blockIdx.x * kMoveThreads + threadIdx.x; base < total; base += stride * kUnroll) {
-    uint4 v[kUnroll];
-    float sc[kUnroll];
-    int idx[kUnroll];
+  const int nw = gridDim.x * 4;
+  const int l = lane_id();
+  for (int r = blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += nw) {
+    int s = src ? src[r] : r;
+    s = min(max(s, 0), n_src_max - 1);
+    const int srow = min(s / div, n_in - 1);
+    const float sc = scale ? scale[scale_by_src ? s : r] : 1.f;
+    const uint4* irow = in + (int64_t)srow * cpr;
+    uint4* orow = out + (int64_t)r * cpr;
+    for (int c0 = 0; c0 < cpr; c0 += 64 * kGatherUnroll) {
+      uint4 v[kGatherUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      idx[u] = base + u * stride;
-      sc[u] = 1.f;
-      if (idx[u] < total) {
-        const int r = idx[u] / cpr;
-        const int c = idx[u] - r * cpr;
-        int s = src ? src[r] : r;
-        s = min(max(s, 0), n_src_max - 1);
-        const int srow = min(s / div, n_in - 1);
-        v[u] = in[(size_t)srow * cpr + c];
-        if (scale) sc[u] = scale[scale_by_src ? s : r];
+      for (int u = 0; u < kGatherUnroll; ++u) {
+        const int c = c0 + 64 * u + l;
+        if (c < cpr) v[u] = irow[c];
       }
-    }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      if (idx[u] < total) {
-        if (scale) {
-          float f[8];
-          unpack8(v[u], f);
+      for (int u = 0; u < kGatherUnroll; ++u) {
+        const int c = c0 + 64 * u + l;
+        if (c < cpr) {
+          uint4 o = v[u];
+          if (scale) {
+            float f[8];
+            unpack8(o, f);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) f[i] *= sc[u];
-          v[u] = pack8(f);
+            for (int i = 0; i < 8; ++i) f[i] *= sc;
+            o = pack8(f);
+          }
+          orow[c] = o;
         }
-        out[idx[u]] = v[u];
       }
     }
   }
@@ -561,9 +557,9 @@ hipError_t launch_gather_rows(const void* in, const int* src, const float* scale
                               bool scale_by_src, int n_in, int n_src_max, int rows,
                               int hidden, int div, void* out, hipStream_t stream) {
   const int cpr = hidden / 8;
-  const int64_t total = (int64_t)rows * cpr;
-  if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL(gather_rows_kernel, dim3(move_grid(total)), dim3(kMoveThreads), 0, stream,
+  if ((int64_t)rows * cpr == 0) return hipSuccess;
+  const int grid = (int)std::min<int64_t>(((int64_t)rows + 3) / 4, 2048);
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(grid), dim3(256), 0, stream,
                      (const uint4*)in, src, scale, scale_by_src ? 1 : 0, n_in, n_src_max, rows,
                      cpr, div, (uint4*)out);
   return hipGetLastError();
