@@ -267,6 +267,40 @@ def test_router_ties(ops):
     np.testing.assert_array_equal(i.cpu().numpy(), [[1, 2, 4], [0, 1, 2]])
 
 
+@pytest.mark.parametrize("T,E,K,func,n_open", [(100, 16, 8, "sigmoid", 4), (77, 128, 8, "softmax", 3),
+                                               (40, 256, 16, "sigmoid", 5)])
+def test_router_masked_experts(ops, T, E, K, func, n_open):
+    """Experts masked by an expert bias of -inf stay pickable after every
+    finite one, in expert-id order: the order of a stable sort of the
+    selection values, the oracle's rule (torch.topk returns -inf entries
+    too).  With K above the number of unmasked experts every pick is still a
+    distinct expert, scored with its unbiased router score.  Both top-k
+    kernels: over given logits, and the fused router (on its own bf16
+    logits; E = 128 and 256 take its full-row path, E = 16 the ragged one)."""
+    rng = np.random.default_rng(E + n_open)
+    bias = np.full(E, -np.inf, np.float32)
+    bias[rng.permutation(E)[:n_open]] = rng.standard_normal(n_open).astype(np.float32) * 0.01
+    norm = True
+    announce(f"router masked experts T={T} E={E} K={K} {func} open={n_open}")
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    s, i = ops.router_topk(f32_dev(logits), K, func, norm, expert_bias=f32_dev(bias))
+    rs, ri = O.router_topk(logits, K, func, norm, expert_bias=bias)
+    got = i.cpu().numpy()
+    np.testing.assert_array_equal(got, ri)
+    assert all(len(set(r)) == K for r in got.tolist())
+    np.testing.assert_allclose(s.cpu().numpy(), rs, rtol=2e-6, atol=1e-7)
+    D = 256
+    x = rand_bf16(rng, (T, D))
+    w = rand_bf16(rng, (E, D), 0.05)
+    s, i, lg = ops.router_fused(bf16_dev(x), bf16_dev(w), K, func, norm, expert_bias=f32_dev(bias),
+                                return_logits=True)
+    rs, ri = O.router_topk(to_np(lg), K, func, norm, expert_bias=bias)
+    got = i.cpu().numpy()
+    np.testing.assert_array_equal(got, ri)
+    assert all(len(set(r)) == K for r in got.tolist())
+    np.testing.assert_allclose(s.cpu().numpy(), rs, rtol=1e-5, atol=1e-7)
+
+
 def _bf16_ulp(v):
     e = np.floor(np.log2(np.maximum(np.abs(v), 1e-30)))
     return np.exp2(e - 7)

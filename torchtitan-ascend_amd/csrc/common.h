@@ -103,6 +103,17 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v + dpp_f<kDppMirror>(v);
 }
 
+// Order-preserving unsigned key of a router selection value: a larger value
+// has a larger key, -inf the smallest of any number, NaN below it (key 1),
+// and 0 is left for a slot already picked.  -0 becomes +0 first (the two
+// compare equal).  Picking the largest key, ties to the lower expert id, is
+// the order of a stable sort of the values, descending, NaN last.
+__device__ __forceinline__ uint32_t sel_key(float v) {
+  const uint32_t b = __float_as_uint(v + 0.f);
+  const uint32_t k = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+  return v == v ? k : 1u;
+}
+
 __device__ __forceinline__ uint64_t lanemask_lt() {
   const int l = lane_id();
   return (l == 0) ? 0ull : (~0ull >> (64 - l));

@@ -174,15 +174,7 @@ struct RouterTopkArgs {
   int nchunks, chunk;
 };
 
-// Order-preserving unsigned key of a selection value: a larger value has a
-// larger key.  The selection is a strict '>' scan that starts from -inf, so
-// -inf and NaN are never picked: both map to 0, the key of a slot already
-// picked.  -0 becomes +0 first (they compare equal as floats).
-__device__ __forceinline__ uint32_t sel_key(float v) {
-  const uint32_t b = __float_as_uint(v + 0.f);
-  const uint32_t k = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
-  return v > -INFINITY ? k : 0u;
-}
+// sel_key (common.h) orders the selection values; a picked slot gets key 0.
 
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
@@ -211,7 +203,8 @@ __device__ __forceinline__ uint32_t row16_umin(uint32_t v) {
 //
 // Selection: each of the K rounds takes the largest key of the row (DPP
 // max), then the lowest expert id holding it (DPP min) -- the (value desc,
-// id asc) order of a stable top-k -- and clears that slot.  The picked
+// id asc) order of a stable top-k, -inf after every finite value and NaN
+// last -- and clears that slot.  The picked
 // scores reach their output lanes through LDS and are summed in pick order
 // for the renormalisation.
 template <int PL, bool FULL>
@@ -303,7 +296,6 @@ __global__ __launch_bounds__(256) void router_topk_partials_kernel(const RouterT
 #pragma unroll
   for (int m = 0; m < PL; ++m) key[m] = live(m) ? sel_key(a.bias ? sc[m] + a.bias[eid(m)] : sc[m]) : 0u;
   int my_i = 0;
-  bool my_deg = false;
   for (int k = 0; k < a.K; ++k) {
     uint32_t km = key[0];
 #pragma unroll
@@ -313,16 +305,12 @@ __global__ __launch_bounds__(256) void router_topk_partials_kernel(const RouterT
 #pragma unroll
     for (int m = PL - 1; m >= 0; --m) cand = (key[m] == km) ? (uint32_t)eid(m) : cand;
     cand = row16_umin(cand);
-    // km == 0: nothing pickable is left (K > the finite scores): expert E - 1
-    // with score 0
-    const bool deg = km == 0u;
-    const int win = deg ? E - 1 : (int)cand;
+    // every expert keeps a key >= 1 until picked and K <= E, so some slot
+    // holds km; the clamp only keeps the index in range regardless
+    const int win = (int)min(cand, (uint32_t)(E - 1));
 #pragma unroll
     for (int m = 0; m < PL; ++m) key[m] = (eid(m) == win) ? 0u : key[m];
-    if (gi == k) {
-      my_i = win;
-      my_deg = deg;
-    }
+    if (gi == k) my_i = win;
   }
   const bool out = gi < a.K;
   if (a.hist) {
@@ -358,7 +346,7 @@ __global__ __launch_bounds__(256) void router_topk_partials_kernel(const RouterT
     }
   }
   lds_wait();
-  const float my_v = (out && !my_deg) ? srow[my_i] : 0.f;
+  const float my_v = out ? srow[my_i] : 0.f;
   lpick[tl][gi] = my_v;
   lds_wait();
   float picked = 0.f;

@@ -794,7 +794,9 @@ hipError_t launch_group_labels(const int* counts_group, int G, int E_loc, int ro
 
 // ---------------------------------------------------------------------------
 // Router top-k: one wave per token.  Each lane holds ceil(E/64) scores in
-// registers; k rounds of a wave-wide (value desc, index asc) argmax.
+// registers; k rounds of a wave-wide argmax of the selection keys (sel_key:
+// value desc, -inf after every finite value, NaN last), ties to the lower
+// expert id.
 // ---------------------------------------------------------------------------
 constexpr int kTopkMaxPerLane = 16;  // E <= 1024
 
@@ -808,7 +810,7 @@ __global__ __launch_bounds__(kMoveThreads) void router_topk_kernel(
   const int l = lane_id();
   for (int t = wave; t < T; t += nwaves) {
     const float* row = logits + (size_t)t * E;
-    float sc[PER_LANE], sel[PER_LANE];
+    float sc[PER_LANE];
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < PER_LANE; ++i) {
@@ -834,32 +836,35 @@ __global__ __launch_bounds__(kMoveThreads) void router_topk_kernel(
 #pragma unroll
       for (int i = 0; i < PER_LANE; ++i) sc[i] = 1.f / (1.f + expf(-sc[i]));
     }
+    // selection keys (sel_key: value desc, -inf after every finite value,
+    // NaN last; 0 = not pickable)
+    uint32_t key[PER_LANE];
 #pragma unroll
     for (int i = 0; i < PER_LANE; ++i) {
       const int e = i * kWave + l;
-      sel[i] = (e < E) ? (bias ? sc[i] + bias[e] : sc[i]) : -INFINITY;
+      key[i] = (e < E) ? sel_key(bias ? sc[i] + bias[e] : sc[i]) : 0u;
     }
     float picked_sum = 0.f;
     float my_val = 0.f;
     int my_idx = 0;
     for (int k = 0; k < K; ++k) {
-      // lane-local best (value desc, index asc)
-      float bv = -INFINITY;
+      // lane-local best (key desc, index asc)
+      uint32_t bk = 0u;
       int bi = 0x7fffffff;
 #pragma unroll
       for (int i = 0; i < PER_LANE; ++i) {
         const int e = i * kWave + l;
-        if (e < E && (sel[i] > bv || (sel[i] == bv && e < bi))) {
-          bv = sel[i];
+        if (key[i] > bk) {  // slots in increasing e: the first maximum is the lowest id
+          bk = key[i];
           bi = e;
         }
       }
 #pragma unroll
       for (int off = kWave / 2; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(bv, off, kWave);
+        const uint32_t ok = (uint32_t)__shfl_xor((int)bk, off, kWave);
         const int oi = __shfl_xor(bi, off, kWave);
-        if (ov > bv || (ov == bv && oi < bi)) {
-          bv = ov;
+        if (ok > bk || (ok == bk && oi < bi)) {
+          bk = ok;
           bi = oi;
         }
       }
@@ -873,7 +878,7 @@ __global__ __launch_bounds__(kMoveThreads) void router_topk_kernel(
       v = __shfl(v, owner, kWave);
 #pragma unroll
       for (int i = 0; i < PER_LANE; ++i)
-        if (i == slot && l == owner) sel[i] = -INFINITY;
+        if (i == slot && l == owner) key[i] = 0u;
       if (bi >= E) bi = 0;  // unreachable when K <= E; keeps the index in range
       picked_sum += v;
       if (l == k) {
