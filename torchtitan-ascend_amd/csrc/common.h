@@ -62,6 +62,16 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
   return v;
 }
 
+// Streaming (non-temporal) 16-byte load and store, for data a kernel reads
+// or writes exactly once.
+__device__ __forceinline__ uint4 load_stream(const uint4* p) {
+  const u32x4_t q = __builtin_nontemporal_load((const u32x4_t*)p);
+  return make_uint4(q[0], q[1], q[2], q[3]);
+}
+__device__ __forceinline__ void store_stream(uint4* p, const uint4& v) {
+  __builtin_nontemporal_store(u32x4_t{v.x, v.y, v.z, v.w}, (u32x4_t*)p);
+}
+
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
 // The wave's LDS writes (and reads) issued so far have completed.  A wave

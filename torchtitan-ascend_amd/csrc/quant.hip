@@ -84,7 +84,8 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint4* __restr
 #pragma unroll
     for (int it = 0; it < kMaxSteps; ++it) {
       const int c = l + 64 * it;
-      v[it] = (c < kv) ? irow[c] : make_uint4(0u, 0u, 0u, 0u);
+      // the row is read once: streaming load (C5 gather + quantise 161 -> 153 us)
+      v[it] = (c < kv) ? load_stream(&irow[c]) : make_uint4(0u, 0u, 0u, 0u);
     }
 #pragma unroll
     for (int it = 0; it < kMaxSteps; ++it) {
