@@ -85,9 +85,13 @@ def _router_setup(ctx, inputs, output):
     _, idx, logits = output
     ctx.save_for_backward(x, w_router, idx, logits)
     ctx.cfg = (func, norm, scale, eps)
+    # the logits are returned for the backward only: no zero gradient for them
+    ctx.set_materialize_grads(False)
 
 
 def _router_bwd(ctx, g_scores, _g_idx, _g_logits):
+    if g_scores is None:
+        return None, None, None, None, None, None, None, None
     x, w_router, idx, logits = ctx.saved_tensors
     func, norm, scale, eps = ctx.cfg
     dx, dw = router_backward(g_scores.contiguous(), idx, logits, x, w_router, func, norm, scale, eps)
@@ -222,9 +226,14 @@ def _experts_setup(ctx, inputs, output):
     ctx.save_for_backward(routed, h, a, w13, w2, offs)
     ctx.limit = limit
     ctx.keep = keep
+    # h and a are outputs for the backward only: autograd must not fill
+    # zero gradients for them ([M, 2H] + [M, H] bf16 per call)
+    ctx.set_materialize_grads(False)
 
 
 def _experts_bwd(ctx, dy, _dh, _da):
+    if dy is None:
+        return None, None, None, None, None, None
     routed, h, a, w13, w2, offs = ctx.saved_tensors
     if not ctx.keep:
         raise RuntimeError("ttamd::experts ran without keep_activations=True; its backward needs h and a")
@@ -356,9 +365,12 @@ def _(rows, sorted_indices):
 
 def _permute_setup(ctx, inputs, output):
     ctx.save_for_backward(output[1])
+    ctx.set_materialize_grads(False)
 
 
 def _permute_bwd(ctx, g_permuted, _g_idx):
+    if g_permuted is None:
+        return None, None, None
     (sorted_indices,) = ctx.saved_tensors
     return token_unpermute(g_permuted, sorted_indices), None, None
 
