@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from conftest import golden_names, load_golden
-from gpu_util import DEV, announce, bf16_dev, f32_dev, rand_bf16, to_np, topk_labels, zipf_counts, labels_from_counts
+from gpu_util import DEV, announce, bf16_dev, edge_rows, f32_dev, rand_bf16, to_np, topk_labels, zipf_counts, labels_from_counts
 from oracle import moe_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -182,6 +182,36 @@ def test_regroup_permute_matches_reference_semantics(pkg):
     np.testing.assert_array_equal(ntpe.cpu().numpy(), ref_n)
     back = disp._unpermute(permuted, shape, pidx)
     np.testing.assert_array_equal(to_np(back), x)
+
+
+def test_regroup_permute_full_size_c4(pkg):
+    """The expert-parallel regroup at C4's full size: M = 32768 rows of
+    D = 7168 received from ep = 8 ranks for 32 local experts (Zipf(1.2) loads,
+    four experts empty), NpuTokenDispatcher._permute's contract
+    (npu_permute.py:63-85).  The permuted indices equal the oracle's stable
+    order bit for bit, the rows at every expert-segment edge plus a random
+    sample moved bit for bit, and each column's sum of the bf16 bit patterns
+    (an integer checksum of all rows, invariant under any permutation) is
+    unchanged."""
+    rng = np.random.default_rng(21)
+    ep, E_loc, M, D = 8, 32, 32768, 7168
+    counts = zipf_counts(M, E_loc, 1.2, 28, rng)
+    counts_group = np.stack([rng.multinomial(int(n), np.full(ep, 1.0 / ep)) for n in counts], axis=1).reshape(-1)
+    gen = torch.Generator(device=DEV).manual_seed(21)
+    x = torch.randn(M, D, device=DEV, generator=gen).to(torch.bfloat16)
+    disp = pkg.HipTokenDispatcher.Config(num_experts=E_loc * ep, top_k=1).build()
+    announce(f"regroup permute full size M={M} D={D} ep={ep} E_loc={E_loc}")
+    _, permuted, pidx, ntpe = disp._permute(x, torch.from_numpy(counts_group).to(DEV), ep, E_loc)
+    ref_s = O.stable_order(O.group_labels(counts_group, E_loc, M), E_loc)
+    got_s = pidx.cpu().numpy()
+    np.testing.assert_array_equal(got_s, ref_s)
+    np.testing.assert_array_equal(ntpe.cpu().numpy(), counts)
+    rows = np.unique(np.concatenate([edge_rows(np.cumsum(counts)), rng.choice(M, 256, replace=False)]))
+    ri = torch.from_numpy(rows).to(DEV)
+    src = torch.from_numpy(ref_s[rows].astype(np.int64)).to(DEV)
+    assert torch.equal(permuted[ri], x[src])
+    colsum = lambda t: t.view(torch.int16).to(torch.int64).sum(0)  # noqa: E731
+    assert torch.equal(colsum(permuted), colsum(x))
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
