@@ -28,7 +28,8 @@
 //     permutation is applied to the global addresses.
 //   * MFMA fragments are read one k16 step ahead; the single barrier of a
 //     stage sits before its last k16 step, after the last reads of the stage,
-//     and is where the next-but-one stage is issued into the freed buffer.
+//     and is where the next-but-one stage's weight rows are issued into the
+//     freed buffer; its token rows follow one k16 step later.
 //   * Per tile, a wave-uniform byte base (SGPRs) plus one 32-bit per-lane
 //     offset per DMA instruction; per stage only the k offset changes.
 //   * Persistent: one workgroup per CU walks the tile list with stride
@@ -203,15 +204,20 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     }
     d_r = r;
   };
-  auto issue = [&](int s) {
+  // A stage's DMA is issued in two parts: the weight rows (P) at the stage
+  // barrier that frees their buffer, the token rows (Q) one k16 step later
+  // (see the k loop).  issue_p sets the stage's bases, which issue_q reads.
+  uint64_t d_spb = 0, d_sqb = 0;
+  uint32_t d_sst = 0;
+  auto issue_p = [&](int s) {
     const int sc = min(s, total - 1);  // past the end: re-load the last stage
     const int r = sc / ksteps;
     const int ks = sc - r * ksteps;
     if (r != d_r) dma_tile(r);
-    const uint64_t pb = d_pbase + (PT ? (uint64_t)ks * TK * a.ldp * 2 : (uint64_t)ks * ROW_BYTES);
-    const uint64_t qb = d_qbase + (uint64_t)ks * ROW_BYTES;
-    const uint32_t st = lds0 + (uint32_t)((s & 1) * STAGE_BYTES) + w * 1024;
-    const uint32_t ldp2 = (uint32_t)a.ldp * 2u, ldq2 = (uint32_t)a.ldq * 2u;
+    d_spb = d_pbase + (PT ? (uint64_t)ks * TK * a.ldp * 2 : (uint64_t)ks * ROW_BYTES);
+    d_sqb = d_qbase + (uint64_t)ks * ROW_BYTES;
+    d_sst = lds0 + (uint32_t)((s & 1) * STAGE_BYTES) + w * 1024;
+    const uint32_t ldp2 = (uint32_t)a.ldp * 2u;
 #pragma unroll
     for (int i = 0; i < DMA_P; ++i) {
       uint32_t voff;
@@ -225,17 +231,24 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
       } else {
         voff = (uint32_t)min(rr0 + 64 * i, d_pmax) * ldp2 + lch16;
       }
-      dma16(voff, pb, st + i * (WAVES * 1024));
+      dma16(voff, d_spb, d_sst + i * (WAVES * 1024));
     }
-    // Token rows past the tile's last 32-row block are never read: skip
-    // their DMA (wave-uniform: instruction i moves row block WAVES * i + w).
+  };
+  // Token rows past the tile's last 32-row block are never read: skip
+  // their DMA (wave-uniform: instruction i moves row block WAVES * i + w).
+  auto issue_q = [&]() {
+    const uint32_t ldq2 = (uint32_t)a.ldq * 2u;
 #pragma unroll
     for (int i = 0; i < DMA_Q; ++i) {
       if (WAVES * i + w < d_qblk8) {
         const uint32_t voff = GATHER ? d_gqoff[GATHER ? i : 0] : (uint32_t)min(rr0 + 64 * i, d_qmax) * ldq2 + lch16;
-        dma16(voff, qb, st + P_BYTES + i * (WAVES * 1024));
+        dma16(voff, d_sqb, d_sst + P_BYTES + i * (WAVES * 1024));
       }
     }
+  };
+  auto issue = [&](int s) {
+    issue_p(s);
+    issue_q();
   };
 
   // ---- fragment geometry -------------------------------------------------------
@@ -331,10 +344,15 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     };
     // One stage: k16 steps 0..3, each computed from registers while the next
     // is read.  Before step 3 every wave has read all of stage s; the barrier
-    // there also waits for stage s + 1 (the only stage in flight), and stage
-    // s + 2 is issued into stage s's buffer.  Every wave runs the same
-    // barrier sequence whatever its block count.
+    // there also waits for stage s + 1 (the only stage in flight), and the
+    // weight rows of stage s + 2 are issued into stage s's buffer at once;
+    // its token rows follow one k16 step later, at the start of stage s + 1
+    // (both have landed by that stage's barrier).  A tile's last stage
+    // issues the whole next-but-one stage at its barrier, before the
+    // epilogue.  Every wave runs the same barrier sequence whatever its
+    // block count.
     for (int ks = 0; ks + 1 < ksteps; ++ks, ++s) {
+      if (ks > 0) issue_q();
       read_frag(f1, s, 1, njv);
       mfma(f0);
       read_frag(f0, s, 2, njv);
@@ -342,12 +360,13 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
       read_frag(f1, s, 3, njv);
       mfma(f0);
       wait_vm_barrier<0>();
-      issue(s + 2);
+      issue_p(s + 2);
       read_frag(f0, s + 1, 0, njv);
       mfma(f1);
     }
     // Last stage of the tile: the next tile's first fragments are read at
     // the start of that tile, with its block count.
+    if (ksteps > 1) issue_q();
     read_frag(f1, s, 1, njv);
     mfma(f0);
     read_frag(f0, s, 2, njv);
