@@ -36,8 +36,9 @@
 //     every wave issues the same DMA count; all read wave 4's).  At the top
 //     of stage s every wave waits for stage s (the only one in flight) and
 //     passes the barrier, which also means stage s - 1 has been read, and
-//     stage s + 1 is issued into its buffer: one stage ahead keeps the
-//     bounding DMA stream busy.
+//     stage s + 1's weight rows are issued into its buffer (its token rows
+//     and scales after the first token block's MFMAs): one stage ahead
+//     keeps the bounding DMA stream busy.
 //   * Persistent workgroups, XCD-aware slots, flattened (tile, stage) DMA
 //     stream and the EPI_SCATTER metadata in LDS follow gemm_fwd.hip.
 #include "common.h"
@@ -161,13 +162,20 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
     }
     d_r = r;
   };
-  auto issue = [&](int s) {
+  // A stage's weight rows are issued at the barrier that frees their buffer,
+  // its token rows and scales after the first token block's MFMAs (see the
+  // k loop); issue_p sets the stage's bases, which issue_q reads.
+  uint64_t d_sqb = 0;
+  uint32_t d_sst = 0;
+  int d_sks = 0;
+  auto issue_p = [&](int s) {
     const int r = s / ksteps;
     const int ks = s - r * ksteps;
     if (r != d_r) dma_tile(r);
     const uint64_t pb = d_pbase + (uint64_t)ks * TKB;
-    const uint64_t qb = d_qbase + (uint64_t)ks * TKB;
-    const uint32_t st = lds0 + (uint32_t)((s % NSTAGE) * STAGE_BYTES);
+    d_sqb = d_qbase + (uint64_t)ks * TKB;
+    d_sst = lds0 + (uint32_t)((s % NSTAGE) * STAGE_BYTES);
+    d_sks = ks;
 #pragma unroll
     for (int i = 0; i < DMA_P; ++i) {
       int prow;  // weight row relative to d_pbase
@@ -175,12 +183,14 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
         prow = (i < 2) ? min(rr0 + 64 * i, d_hmax) : (int)a.hidden + min(rr0 + 64 * (i - 2), d_hmax);
       else
         prow = min(rr0 + 64 * i, d_pmax);
-      dma16((uint32_t)(prow * a.ldp) + lch16, pb, st + w * 1024 + i * (WAVES * 1024));
+      dma16((uint32_t)(prow * a.ldp) + lch16, pb, d_sst + w * 1024 + i * (WAVES * 1024));
     }
+  };
+  auto issue_q = [&]() {
 #pragma unroll
     for (int i = 0; i < DMA_Q; ++i)
-      dma16((uint32_t)(min(rr0 + 64 * i, d_qmax) * a.ldq) + lch16, qb, st + P_BYTES + w * 1024 + i * (WAVES * 1024));
-    dma4(d_scoff, d_scbase + (uint64_t)ks * d_scstep, st + d_sclds);
+      dma16((uint32_t)(min(rr0 + 64 * i, d_qmax) * a.ldq) + lch16, d_sqb, d_sst + P_BYTES + w * 1024 + i * (WAVES * 1024));
+    dma4(d_scoff, d_scbase + (uint64_t)d_sks * d_scstep, d_sst + d_sclds);
   };
 
   // ---- fragment geometry -------------------------------------------------------
@@ -205,7 +215,8 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
   auto sw_lane = [&](int pb) { return (EPI == EPI_SWIGLU) ? (pb < 2 ? 0 : 1 + wp) : (wp >> 1); };
 
   // ---- prologue: stage 0 in flight ----------------------------------------------
-  issue(0);
+  issue_p(0);
+  issue_q();
 
   int s = 0;
   for (int r = 0; r < nmy; ++r) {
@@ -228,7 +239,8 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
       // with stage s - 1: its buffer takes stage s + 1.  The DMA stream is
       // the bound, so one stage ahead keeps it busy.
       wait_vm_barrier<0>();
-      if (s + 1 < total) issue(s + 1);
+      const bool more = s + 1 < total;
+      if (more) issue_p(s + 1);
       const char* st = smem + (s % NSTAGE) * STAGE_BYTES;
       i32x8_t fa[NPB16];
       // A block's weight scale is one value for the whole wave (every lane
@@ -271,6 +283,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
         if (jb > 0) scale_add(jb - 1, sx_prev);
         sx_prev = sxv[jb % NBS];
         if (jb + 2 < NJ16) read_b(jb + 2);
+        if (jb == 0 && more) issue_q();  // (later placements spill)
       }
       scale_add(NJ16 - 1, sx_prev);
     }
