@@ -36,9 +36,13 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
 // fp32 -> bf16 (round to nearest even) -> fp32.
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
-// Pack two floats into one dword of two bf16 (lo in bits 0..15).
+// Pack two floats into one dword of two bf16 (lo in bits 0..15).  The
+// two-wide conversion is one v_cvt_pk_bf16_f32 with both sources; two
+// scalar casts cost two conversions, a shift and an or.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 
 // Unpack 8 bf16 held in a uint4 into 8 floats.
