@@ -472,21 +472,39 @@ __global__ __launch_bounds__(256) void router_backward_kernel(const RouterBwdArg
 }
 
 // w_pad [ldd rows][D] = w_router rows, then zero rows; offs1[0] = T (one
-// expert owning every token row, for the padded GEMMs).
+// expert owning every token row, for the padded dgrad); offsg[g] = the end of
+// token group g of G near-equal groups (the weight gradient's partial sums).
 __global__ __launch_bounds__(256) void router_pad_kernel(const uint4* __restrict__ w, int E, int ldd, int cpr,
-                                                         uint4* __restrict__ w_pad, int* offs1, int T) {
+                                                         uint4* __restrict__ w_pad, int* offs1, int T, int* offsg,
+                                                         int G) {
   const int total = ldd * cpr;
   for (int i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256)
     w_pad[i] = (i / cpr < E) ? w[i] : make_uint4(0, 0, 0, 0);
-  if (blockIdx.x == 0 && threadIdx.x == 0) offs1[0] = T;
+  if (blockIdx.x == 0) {
+    if (threadIdx.x == 0) offs1[0] = T;
+    for (int g = threadIdx.x; g < G; g += 256) offsg[g] = (int)((int64_t)T * (g + 1) / G);
+  }
 }
 
-// dw[E][D] (fp32 or bf16) = the first E rows of the padded fp32 gradient.
-__global__ __launch_bounds__(256) void router_dw_copy_kernel(const float* __restrict__ src, int n, void* dst,
-                                                             int fp32) {
+// dw[e][d] (fp32 or bf16) = sum over the G token groups of part[g][e][d], in
+// group order (deterministic).  part rows are n_part >= E wide.
+__global__ __launch_bounds__(256) void router_dw_reduce_kernel(const float4* __restrict__ part, int G, int n_part,
+                                                               int E, int D4, void* dst, int fp32) {
+  const int n = E * D4;
+  const int64_t gstride = (int64_t)n_part * D4;
   for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
-    if (fp32) ((float*)dst)[i] = src[i];
-    else ((bf16_t*)dst)[i] = (bf16_t)f32_to_bf16(src[i]);
+    float4 acc = part[i];
+    for (int g = 1; g < G; ++g) {
+      const float4 v = part[g * gstride + i];
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
+    }
+    if (fp32)
+      ((float4*)dst)[i] = acc;
+    else
+      ((uint2*)dst)[i] = make_uint2(pack_bf16x2(acc.x, acc.y), pack_bf16x2(acc.z, acc.w));
   }
 }
 
@@ -592,17 +610,29 @@ static_assert(kRouterMaxE == 256, "EB = 8 covers 256 experts");
 
 // ---------------------------------------------------------------------------
 // Router backward: d(logits) (kernel above), then dx = dlogits . W_r and
-// dW_r = dlogits^T . x on the grouped GEMM kernels as one expert, with the
+// dx = dlogits . w_router on the grouped dgrad kernel as one expert, with the
 // expert count padded to a multiple of 128 (zero logit-gradient columns and
-// zero weight rows contribute nothing).
+// zero weight rows contribute nothing).  dW_r = dlogits^T . x on the wgrad
+// kernel with the T tokens split into G groups as its "experts": G partial
+// [E][D] sums, then one pass adds them in group order.  One group would leave
+// the launch with D / 256 tiles (20 of 256 CUs at D = 5120).
 // ---------------------------------------------------------------------------
 static int router_pad_e(int E) { return (E + 127) & ~127; }
+static int router_dw_rows(int E) { return E < 8 ? 8 : (E + 7) & ~7; }  // the wgrad's dy columns read (>= 8)
+static int router_dw_groups(int64_t T, int E, int64_t D) {
+  const int tiles = ((router_dw_rows(E) + 255) / 256) * (int)((D + 255) / 256);
+  int g = 256 / tiles;  // about one tile per CU of an MI355X
+  g = g < 1 ? 1 : (g > 32 ? 32 : g);
+  const int64_t by_rows = T / 256;  // at least 256 rows (4 stages) per group
+  return (int)(by_rows < 1 ? 1 : (g < by_rows ? g : by_rows));
+}
 static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 size_t router_backward_workspace_bytes(int64_t T, int E, int64_t D) {
   const int64_t P = router_pad_e(E);
-  return al256((size_t)T * P * 2) + al256((size_t)P * D * 2) + al256((size_t)P * D * 4) + al256(16) +
-         al256(gemm_workspace_bytes(T, 1));
+  const int64_t G = router_dw_groups(T, E, D);
+  return al256((size_t)T * P * 2) + al256((size_t)P * D * 2) + al256((size_t)G * router_dw_rows(E) * D * 4) +
+         al256(16) + al256((size_t)G * 4) + al256(gemm_workspace_bytes(T, 1));
 }
 
 hipError_t launch_router_backward(const float* grad, const int64_t* idx, const void* logits, const void* x,
@@ -611,15 +641,19 @@ hipError_t launch_router_backward(const float* grad, const int64_t* idx, const v
                                   void* ws, hipStream_t stream) {
   if (T == 0) return hipSuccess;
   const int P = router_pad_e(E);
+  const int G = router_dw_groups(T, E, D);
+  const int NR = router_dw_rows(E);
   char* p = (char*)ws;
   bf16_t* dlog = (bf16_t*)p;
   p += al256((size_t)T * P * 2);
   bf16_t* w_pad = (bf16_t*)p;
   p += al256((size_t)P * D * 2);
-  float* dw_pad = (float*)p;
-  p += al256((size_t)P * D * 4);
+  float* dw_part = (float*)p;
+  p += al256((size_t)G * NR * D * 4);
   int* offs1 = (int*)p;
   p += al256(16);
+  int* offsg = (int*)p;
+  p += al256((size_t)G * 4);
   void* gws = p;
 
   RouterBwdArgs b;
@@ -645,24 +679,34 @@ hipError_t launch_router_backward(const float* grad, const int64_t* idx, const v
   const int cpr = D / 8;
   const int pg = min(2048, (P * cpr + 255) / 256);
   hipLaunchKernelGGL(router_pad_kernel, dim3(pg), dim3(256), 0, stream, (const uint4*)w, E, P, cpr, (uint4*)w_pad,
-                     offs1, T);
+                     offs1, T, offsg, G);
   if ((err = hipGetLastError()) != hipSuccess) return err;
   if (dx) {
     // dx[t][d] = sum_e dlogits[t][e] w[e][d]: dgrad with the weight [1][P][D]
     if ((err = launch_grouped_mm_dgrad(dlog, w_pad, offs1, T, 1, P, D, dx, gws, stream)) != hipSuccess) return err;
   }
   if (dw) {
-    // dw[e][d] = sum_t dlogits[t][e] x[t][d]: wgrad over the one expert
-    const bool direct = (P == E) && dw_fp32;
-    if ((err = launch_grouped_mm_wgrad(dlog, x, offs1, T, 1, P, D, direct ? dw : (void*)dw_pad, true, stream)) !=
-        hipSuccess)
-      return err;
-    if (!direct) {
-      const int n = E * D;
-      hipLaunchKernelGGL(router_dw_copy_kernel, dim3(min(2048, (n + 255) / 256)), dim3(256), 0, stream, dw_pad, n,
-                         dw, dw_fp32 ? 1 : 0);
-      err = hipGetLastError();
-    }
+    // dw_part[g][e][d] = sum over the tokens t of group g of dlogits[t][e] x[t][d]
+    // (columns E..NR-1 of dlogits are the zero padding)
+    WgradDmaArgs wa = {};
+    wa.dy = dlog;
+    wa.lddy = P;
+    wa.x = (const bf16_t*)x;
+    wa.ldx = D;
+    wa.offs = offsg;
+    wa.E = G;
+    wa.M = T;
+    wa.N = NR;
+    wa.K = D;
+    wa.n_tiles = (NR + 255) / 256;
+    wa.k_tiles = (D + 255) / 256;
+    wa.dw = dw_part;
+    wa.dw_fp32 = 1;
+    if ((err = launch_wgrad_dma(wa, stream)) != hipSuccess) return err;
+    const int n4 = E * (D / 4);
+    hipLaunchKernelGGL(router_dw_reduce_kernel, dim3(min(2048, (n4 + 255) / 256)), dim3(256), 0, stream,
+                       (const float4*)dw_part, G, NR, E, D / 4, dw, dw_fp32 ? 1 : 0);
+    err = hipGetLastError();
   }
   return err;
 }
