@@ -240,31 +240,47 @@ __global__ __launch_bounds__(THREADS, 1) void gg_wgrad_dma_kernel(const WgradDma
     int er32 = l & 31;
     asm volatile("" : "+v"(er32));
     const int half = l >> 5;
+    // Both forms go through the wave's private 4 KB LDS slab (row r: 128
+    // bytes, 16-byte chunk c at c ^ (r & 7)) and leave as streaming stores
+    // of 8 whole 128-byte rows per instruction: the gradient is written once
+    // and not read here again, and cached it would evict the operand lines
+    // the other workgroups of the XCD are about to read (routed C3 dW2 939
+    // -> 788 us).
+    char* slab = smem + LDS_BYTES + w * SLAB_BYTES;
     if (a.dw_fp32) {
+      // fp32: one 32-row x 32-column block (128 bytes per row) at a time
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const int n = t.nt * TQ + brow[j] + er32;
-        const bool n_ok = n < a.N;
-        const int64_t rowoff = ((int64_t)t.e * a.N + n) * a.K;
 #pragma unroll
         for (int pb = 0; pb < NPB; ++pb) {
-          if (t.kt * TP + arow[pb] < a.K) {
+          if (t.kt * TP + arow[pb] < a.K) {  // wave-uniform: the block's 32 columns are valid together
+            const floatx16_t& v = acc[pb][j];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-              const int k = t.kt * TP + arow[pb] + 8 * g + 4 * half;
-              const floatx16_t& v = acc[pb][j];
-              if (n_ok)
-                *(float4*)((float*)a.dw + rowoff + k) = make_float4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
+              const int chunk = (2 * g + half) ^ (er32 & 7);  // columns 8g + 4 half .. + 3
+              *(float4*)(slab + er32 * 128 + chunk * 16) = make_float4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
+            }
+            lds_wait();  // the slab writes have landed
+            uint4 o4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int r = 8 * i + (l >> 3);
+              o4[i] = *(const uint4*)(slab + r * 128 + (((l & 7) ^ (r & 7)) << 4));
+            }
+            lds_wait();  // read before the next block overwrites the slab
+            const int col = t.kt * TP + arow[pb] + 4 * (l & 7);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int n = t.nt * TQ + brow[j] + 8 * i + (l >> 3);
+              if (n < a.N) store_stream((uint4*)((float*)a.dw + ((int64_t)t.e * a.N + n) * a.K + col), o4[i]);
             }
           }
           __builtin_amdgcn_sched_barrier(0);
         }
       }
     } else if (t.kt * TP + arow[0] < a.K) {  // the wave's 64 columns are valid together
-      // bf16: each 32-row block goes through the wave's private 4 KB LDS
-      // slab (row r: 128 bytes, 16-byte chunk c at c ^ (r & 7)) and leaves
-      // as 4 stores of 8 whole 128-byte rows.
-      char* slab = smem + LDS_BYTES + w * SLAB_BYTES;
+      // bf16: one 32-row block (the wave's 64 columns, 128 bytes per row)
+      // at a time
       const int col = t.kt * TP + arow[0] + 8 * (l & 7);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
@@ -290,7 +306,7 @@ __global__ __launch_bounds__(THREADS, 1) void gg_wgrad_dma_kernel(const WgradDma
           const int r = 8 * i + (l >> 3);
           const uint4 o = o4[i];
           const int n = t.nt * TQ + brow[j] + r;
-          if (n < a.N) *(uint4*)((bf16_t*)a.dw + ((int64_t)t.e * a.N + n) * a.K + col) = o;
+          if (n < a.N) store_stream((uint4*)((bf16_t*)a.dw + ((int64_t)t.e * a.N + n) * a.K + col), o);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
