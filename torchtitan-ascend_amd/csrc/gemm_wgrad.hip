@@ -51,6 +51,7 @@ constexpr int SLAB_BYTES = 32 * 128;        // per wave: one 32 x 64 bf16 output
 constexpr int LDS_TOTAL = LDS_BYTES + WAVES * SLAB_BYTES;  // 160 KB
 constexpr int DMA_OP = OP_BYTES / 1024 / WAVES;  // 4 instructions per operand and wave
 constexpr int DMA_PER_STAGE = 2 * DMA_OP;
+constexpr int kStripN = 4;  // n tiles per strip of the tile order
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
@@ -86,8 +87,16 @@ __global__ __launch_bounds__(THREADS, 1) void gg_wgrad_dma_kernel(const WgradDma
     const int id = r * G + slot;
     t.e = id / per_e;
     const int rem = id - t.e * per_e;
-    t.nt = rem / a.k_tiles;
-    t.kt = rem - t.nt * a.k_tiles;
+    // Within an expert, strips of kStripN n tiles, k tile major inside a
+    // strip: an XCD's 32 consecutive slots then cover 4 n x 8 k tiles, so
+    // each dY slice is shared by 8 of its workgroups and each X slice by 4
+    // in its L2 (row-major: one n tile x 32 k tiles, every X slice read by
+    // one workgroup of the XCD).
+    const int strip = rem / (kStripN * a.k_tiles);
+    const int in_strip = rem - strip * kStripN * a.k_tiles;
+    const int gn = min(kStripN, a.n_tiles - strip * kStripN);
+    t.kt = in_strip / gn;
+    t.nt = strip * kStripN + (in_strip - t.kt * gn);
     t.m0 = t.e == 0 ? 0 : sload_int(a.offs + t.e - 1);
     t.m1 = sload_int(a.offs + t.e);
     t.m0 = min(max(t.m0, 0), a.M);
