@@ -23,10 +23,13 @@
 //     form, with no partial sums kept across MFMAs.  The scale FMAs of token
 //     block jb - 1 run under block jb's MFMAs, and with two waves per SIMD
 //     under the other wave's as well.
-//   * The kernel is bound by the L2 -> LDS stream (each CU keeps about 64
-//     line requests in flight), so the tile is as large as the registers
-//     allow: 256 x 256 moves 66 KB per 16.8 MFLOP stage where 256 x 128
-//     moved 48 KB per 8.4.  The 128 accumulators leave room for the 4
+//   * The 256 x 128 tile was bound by the L2 -> LDS stream (each CU keeps
+//     about 64 line requests in flight), so the tile is as large as the
+//     registers allow: 256 x 256 moves 66 KB per 16.8 MFLOP stage where
+//     256 x 128 moved 48 KB per 8.4.  With it a stage's DMA has landed
+//     before the barrier that needs it (~1 % of the stage waiting), and the
+//     stage is the MFMAs, the block-scale FMAs and the fragment reads of the
+//     two waves of each SIMD.  The 128 accumulators leave room for the 4
 //     weight fragments of the stage and only 2 token fragments, read just
 //     before use.
 //   * Two LDS stages of 66 KB: 32 KB weight rows + 32 KB token rows (DMA,
