@@ -117,8 +117,25 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   // XCD-aware slot: hardware block ids go round-robin over the 8 XCDs; give
   // XCD x the slots [x*G/8, (x+1)*G/8) so that it takes consecutive tiles.
   const int slot = (b & 7) * (G >> 3) + (b >> 3);
-  const int ntiles = sload_int(a.n_qtiles) * a.np_tiles;
+  const int nqt = sload_int(a.n_qtiles);
+  const int ntiles = nqt * a.np_tiles;
   const int nmy = slot < ntiles ? (ntiles - slot + G - 1) / G : 0;
+  // Persistent order of the SwiGLU (w13) kernels: token tiles in pairs,
+  // weight tile major inside a pair, so 32 consecutive slots (one XCD's)
+  // take both token tiles of an expert with 16 weight tiles rather than one
+  // token tile with 32: each weight tile is shared in the XCD's L2 instead
+  // of across XCDs (C3 w13 -6 %; the other epilogues' kernels were slower
+  // with it and keep the table order).  Returns the table order's tile id
+  // (qt * np_tiles + pt).
+  auto tile_at = [&](int r) {
+    const int L = r * G + slot;
+    if constexpr (EPI != EPI_SWIGLU) return L;
+    const int blk = L / (2 * a.np_tiles);
+    const int in_blk = L - blk * 2 * a.np_tiles;
+    const int gq = min(2, nqt - 2 * blk);
+    const int pt = in_blk / gq;
+    return (2 * blk + (in_blk - pt * gq)) * a.np_tiles + pt;
+  };
   const int ksteps = a.kred / TK;
   const int total = nmy * ksteps;
   if (total == 0) return;
@@ -133,7 +150,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   // Source-row ids of tile round r (gathered rows only): 64-row chunk c of
   // the tile is moved by wave c % WAVES into slot r % 2.
   auto load_ids = [&](int r) {
-    const int tile = r * G + slot;
+    const int tile = tile_at(r);
     const int4 ti = sload_int4(a.table + tile / a.np_tiles);
     for (int c = w; c < TQ / 64; c += WAVES) {
       const uint32_t q = (uint32_t)min(64 * c + l, ti.z - ti.y - 1);
@@ -156,7 +173,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   uint32_t d_ptoff[PT ? DMA_P : 1];
   uint32_t d_gqoff[GATHER ? DMA_Q : 1];
   auto dma_tile = [&](int r) {
-    const int tile = r * G + slot;
+    const int tile = tile_at(r);
     const int qt = tile / a.np_tiles;
     const int pt = tile - qt * a.np_tiles;
     const int4 ti = sload_int4(a.table + qt);
@@ -560,7 +577,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   };
 
   for (int r = 0; r < nmy; ++r) {
-    const int tile = r * G + slot;
+    const int tile = tile_at(r);
     const int qt = tile / a.np_tiles;
     const int pt = tile - qt * a.np_tiles;
     const int4 ti = sload_int4(a.table + qt);
