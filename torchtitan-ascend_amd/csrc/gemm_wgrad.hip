@@ -20,9 +20,11 @@
 //     transposed reads); one barrier per stage as in gemm_fwd.hip.
 //   * The last stage of an expert reads clamped rows past its end; their
 //     products are removed by zeroing those rows in the x fragments.
-//   * Persistent over (expert, n tile, k tile), expert-major, with the
-//     XCD-aware slot mapping of gemm_fwd.hip; the DMA stream runs over the
-//     flattened (tile, stage) sequence, whose stage counts vary per expert.
+//   * Persistent over (expert, n tile, k tile), expert-major, the n tiles in
+//     strips of 4 with the k tile major inside a strip (see tile_of), with
+//     the XCD-aware slot mapping of gemm_fwd.hip; the DMA stream runs over
+//     the flattened (tile, stage) sequence, whose stage counts vary per
+//     expert.
 //     An expert without rows still takes one (fully masked) stage, so its
 //     gradient tile is written as zeros.
 #include "common.h"
@@ -253,8 +255,8 @@ __global__ __launch_bounds__(THREADS, 1) void gg_wgrad_dma_kernel(const WgradDma
     // bytes, 16-byte chunk c at c ^ (r & 7)) and leave as streaming stores
     // of 8 whole 128-byte rows per instruction: the gradient is written once
     // and not read here again, and cached it would evict the operand lines
-    // the other workgroups of the XCD are about to read (routed C3 dW2 939
-    // -> 788 us).
+    // the other workgroups of the XCD are about to read (routed C3 dW2 934
+    // -> 724 us in bf16).
     char* slab = smem + LDS_BYTES + w * SLAB_BYTES;
     if (a.dw_fp32) {
       // fp32: one 32-row x 32-column block (128 bytes per row) at a time
