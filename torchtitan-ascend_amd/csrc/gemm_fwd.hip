@@ -36,7 +36,8 @@
 //     gridDim.x; the DMA stream runs over the flattened (tile, k-stage)
 //     sequence, so the next tile's first stages load during the current
 //     tile's epilogue.  Within a round the 32 workgroups of one XCD take 32
-//     consecutive tiles (same expert), so the weights are shared in its L2.
+//     consecutive tiles (same expert), so the weights are shared in its L2
+//     (the SwiGLU kernels walk the token tiles in pairs, see tile_at).
 //
 // Reference semantics (torchtitanturbo/models/common/npu_gmm.py):
 //   :17-18, :31, :38  torch._grouped_mm(x, w.transpose(-2, -1), offs)
