@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import DEV, announce, bf16_dev, f32_dev, rand_bf16, to_np, zipf_counts
+from gpu_util import DEV, announce, assert_close, bf16_dev, f32_dev, rand_bf16, to_np, zipf_counts
 from oracle import moe_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -91,6 +91,25 @@ def test_grouped_mm_swiglu(ops, M, E, D, H, kind, limit):
     assert O.max_rel_err(to_np(a), a_ref) < TOL
     # the activation is computed from the bf16 pre-activation the kernel stored
     assert O.max_rel_err(to_np(a), O.swiglu(to_np(h), limit)) < 1e-2
+
+
+@pytest.mark.parametrize("counts,H", [((400, 100), 2304), ((400, 0, 100, 333), 2304), ((50,), 2304)])
+def test_grouped_mm_swiglu_paired_walk_odd_tiles(ops, counts, H):
+    """The SwiGLU kernels walk the token tiles in pairs (weight tile major
+    inside a pair); with an odd token-tile count the last pair has one tile,
+    and with H / 128 = 18 weight tiles a pair spans more than one XCD's 32
+    slots.  Every tile must still be computed exactly once: compared in
+    full with the oracle, per row."""
+    rng = np.random.default_rng(sum(counts) + H)
+    counts = np.array(counts, np.int64)
+    M, E, D = int(counts.sum()), len(counts), 256
+    x = rand_bf16(rng, (M, D))
+    w13 = rand_bf16(rng, (E, 2 * H, D), 0.08)
+    announce(f"swiglu paired walk counts={tuple(counts)} H={H}")
+    a, h = ops.grouped_mm_swiglu(bf16_dev(x), bf16_dev(w13), _offs(counts), None, save_h=True)
+    h_ref = O.bf16_round(_gmm_ref(x, w13, counts))
+    assert_close(to_np(h), h_ref, TOL, "h")
+    assert_close(to_np(a), O.swiglu(h_ref), TOL, "a")
 
 
 @pytest.mark.parametrize("T,K,E,D,H,kind", [(500, 2, 8, 256, 128, "random"), (1024, 4, 16, 512, 192, "zipf"),
