@@ -139,7 +139,7 @@ int ttamd_router_backward(const float* grad_top_scores,
  *   top_scores.view(-1)[sorted_indices[j]]).
  *   tokens_per_expert (nullable, fp32 [E]) += counts: upstream's
  *   load-balancing accumulator (router.tokens_per_expert.add_(histc)).
- *   gemm_plan (nullable, ttamd_gemm_workspace_bytes(T*topk, E) bytes)
+ *   gemm_plan (nullable, ttamd_gemm_plan_bytes(T*topk, E) bytes)
  *   receives the token-tile table of the expert-sorted rows that
  *   ttamd_moe_experts_forward can use for both grouped GEMMs.
  * Same argument limits as ttamd_router_fused; workspace:
@@ -321,8 +321,19 @@ int ttamd_moe_group_labels(const int32_t* counts_group, int num_groups,
  * Grouped GEMMs over ragged expert segments (bf16 in, fp32 accumulate).     *
  * ------------------------------------------------------------------------ */
 
-/* Bytes of device workspace every ttamd_grouped_mm* call needs. */
+/* Bytes of device workspace every ttamd_grouped_mm* call needs: the
+ * tile plan (ttamd_gemm_plan_bytes) followed by the partial sums of the
+ * GEMMs' split leftover tiles (tiles left after the last full round of the
+ * persistent walk are cut along k over the idle CUs; the last piece of a
+ * tile adds the pieces in a fixed order, so results do not depend on which
+ * piece finishes last). */
 size_t ttamd_gemm_workspace_bytes(int64_t num_rows, int num_experts);
+
+/* Bytes of a tile plan (gemm_plan of ttamd_router_route and
+ * ttamd_moe_experts_forward): the token-tile table of num_rows
+ * expert-sorted rows and the split-tile arrival counters.  No counterpart
+ * in the reference, whose grouped GEMM plans inside the operator. */
+size_t ttamd_gemm_plan_bytes(int64_t num_rows, int num_experts);
 
 /*
  * out[m, n] = sum_k x[m, k] * w[e(m), n, k]  (bf16 out).
@@ -404,8 +415,10 @@ int ttamd_grouped_mm_unpermute(const void* a, const void* w2,
  * in [0, E) (offs[E-1] = T * topk).  D % 128 == 0, H % 64 == 0.
  * Without score_before_experts the gather is fused into the w13 GEMM's
  * loads (the routed copy is never written).  gemm_plan (nullable): the tile
- * table from ttamd_router_route for these offs; both GEMMs use it (null:
- * one is built in the workspace).  workspace:
+ * plan from ttamd_router_route for these offs; both GEMMs use it (null:
+ * one is built in the workspace).  Its split-tile counters are counted up
+ * and back to zero by each GEMM, so one plan serves one call at a time.
+ * workspace:
  * ttamd_moe_experts_forward_workspace_bytes (tile table, a, and for
  * score-before the routed rows, for topk > 1 y).
  */
@@ -419,7 +432,7 @@ int ttamd_moe_experts_forward(const void* tokens, int64_t num_tokens,
                               const int32_t* offs, const float* sorted_scores,
                               int score_before_experts, float swiglu_limit,
                               const void* w13, const void* w2, void* out,
-                              const void* gemm_plan, size_t gemm_plan_bytes,
+                              void* gemm_plan, size_t gemm_plan_bytes,
                               void* workspace, size_t workspace_bytes,
                               void* stream);
 

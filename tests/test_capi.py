@@ -102,7 +102,7 @@ def test_router_topk_rejects_bad_k():
     assert "topk" in msg
 
 
-@pytest.mark.parametrize("fn", ["ttamd_route_workspace_bytes", "ttamd_gemm_workspace_bytes"])
+@pytest.mark.parametrize("fn", ["ttamd_route_workspace_bytes", "ttamd_gemm_workspace_bytes", "ttamd_gemm_plan_bytes"])
 def test_workspace_queries_reject_negative(fn):
     assert getattr(_lib.load(), fn)(-1, 4) == 0
 

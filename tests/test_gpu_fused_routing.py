@@ -47,10 +47,16 @@ def plan_table(counts: np.ndarray, M: int, max_rows: int = 320) -> tuple[int, np
     return i, tab
 
 
+# plan layout: int4 header {count, ...}, 512 split-tile counters, the table
+SPLIT_TILES = 512
+TABLE_OFF = 16 + 4 * SPLIT_TILES
+
+
 def _plan_of(plan: torch.Tensor, M: int, E: int) -> tuple[int, np.ndarray]:
     raw = plan.cpu().numpy()
     max_tiles = M // 128 + E + 1
-    return int(raw[:4].view(np.int32)[0]), raw[16:16 + 16 * max_tiles].view(np.int32).reshape(max_tiles, 4)
+    assert not raw[16:TABLE_OFF].any(), "split-tile counters must be zero"
+    return int(raw[:4].view(np.int32)[0]), raw[TABLE_OFF:TABLE_OFF + 16 * max_tiles].view(np.int32).reshape(max_tiles, 4)
 
 
 ROUTER_CASES = [

@@ -270,9 +270,9 @@ int ttamd_router_route(const void* x, const void* w_router, const float* expert_
   TRY(check_ws(fn, workspace, workspace_bytes, ttamd_router_route_workspace_bytes(num_tokens, num_experts, dim, topk)));
   if (gemm_plan) {
     REQUIRE(aligned16(gemm_plan), "%s: gemm_plan must be 16-byte aligned", fn);
-    REQUIRE(gemm_plan_bytes >= ttamd::gemm_workspace_bytes(M, num_experts),
+    REQUIRE(gemm_plan_bytes >= ttamd::gemm_plan_bytes(M, num_experts),
             "%s: gemm_plan too small (%zu bytes, need %zu)", fn, gemm_plan_bytes,
-            ttamd::gemm_workspace_bytes(M, num_experts));
+            ttamd::gemm_plan_bytes(M, num_experts));
   }
   hipStream_t s = (hipStream_t)stream;
   int* hist = (int*)((char*)workspace + rbytes);
@@ -296,7 +296,7 @@ size_t ttamd_moe_experts_forward_workspace_bytes(int64_t num_tokens, int64_t dim
 int ttamd_moe_experts_forward(const void* tokens, int64_t num_tokens, int64_t dim, int64_t hidden,
                               int num_experts, int topk, const int32_t* sorted_indices, const int32_t* offs,
                               const float* sorted_scores, int score_before_experts, float swiglu_limit,
-                              const void* w13, const void* w2, void* out, const void* gemm_plan,
+                              const void* w13, const void* w2, void* out, void* gemm_plan,
                               size_t gemm_plan_bytes, void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "ttamd_moe_experts_forward";
   REQUIRE(topk >= 1 && topk <= 64, "%s: topk must be in [1, 64]", fn);
@@ -319,9 +319,9 @@ int ttamd_moe_experts_forward(const void* tokens, int64_t num_tokens, int64_t di
           "%s: score_before_experts needs sorted_scores", fn);
   if (gemm_plan) {
     REQUIRE(aligned16(gemm_plan), "%s: gemm_plan must be 16-byte aligned", fn);
-    REQUIRE(gemm_plan_bytes >= ttamd::gemm_workspace_bytes(M, num_experts),
+    REQUIRE(gemm_plan_bytes >= ttamd::gemm_plan_bytes(M, num_experts),
             "%s: gemm_plan too small (%zu bytes, need %zu)", fn, gemm_plan_bytes,
-            ttamd::gemm_workspace_bytes(M, num_experts));
+            ttamd::gemm_plan_bytes(M, num_experts));
   }
   TRY(check_ws(fn, workspace, workspace_bytes,
                ttamd_moe_experts_forward_workspace_bytes(num_tokens, dim, hidden, num_experts, topk,
@@ -515,6 +515,11 @@ int ttamd_probe_next_gemm(void* start_event, void* end_event) {
 size_t ttamd_gemm_workspace_bytes(int64_t num_rows, int num_experts) {
   if (num_rows < 0 || num_experts < 1) return 0;
   return ttamd::gemm_workspace_bytes(num_rows, num_experts);
+}
+
+size_t ttamd_gemm_plan_bytes(int64_t num_rows, int num_experts) {
+  if (num_rows < 0 || num_experts < 1) return 0;
+  return ttamd::gemm_plan_bytes(num_rows, num_experts);
 }
 
 int ttamd_grouped_mm(const void* x, const void* w, const int32_t* offs, int64_t num_rows,

@@ -24,7 +24,8 @@ namespace ttamd {
 __global__ __launch_bounds__(1024) void tile_map_kernel(const int* __restrict__ offs, int E,
                                                         int M, int max_tiles, int max_rows,
                                                         int4* __restrict__ table,
-                                                        int* __restrict__ count) {
+                                                        int* __restrict__ count,
+                                                        int* __restrict__ split_cnt) {
   __shared__ int sh[1024 / kWave + 1];
   auto range = [&](int e, int& r0, int& r1) {
     // offs == nullptr: one expert owning all M rows
@@ -33,13 +34,13 @@ __global__ __launch_bounds__(1024) void tile_map_kernel(const int* __restrict__ 
     r0 = min(max(a, 0), M);
     r1 = min(max(b, r0), M);
   };
-  block_tile_table<1024>(range, E, max_tiles, max_rows, table, count, sh);
+  block_tile_table<1024>(range, E, max_tiles, max_rows, table, count, split_cnt, sh);
 }
 
 hipError_t launch_tile_map(const int* offs, int E, int M, int max_rows, void* ws, hipStream_t stream) {
   TileTable tt = tile_table_in(ws);
   hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, stream, offs, E, M,
-                     max_row_tiles(M, E), max_rows, tt.table, tt.count);
+                     max_row_tiles(M, E), max_rows, tt.table, tt.count, tt.split_cnt);
   return hipGetLastError();
 }
 
@@ -50,9 +51,20 @@ int gemm_max_qtiles(int M, int E) { return max_row_tiles(M, E); }
 
 int gemm_fwd_tile_rows() { return kFwdTileRows; }
 
-size_t gemm_workspace_bytes(int64_t M, int E) {
-  return (size_t)(max_row_tiles((int)M, E) + 1) * sizeof(int4) + 256;
+static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// The tile plan: header, split-tile counters, tile table.
+size_t gemm_plan_bytes(int64_t M, int E) {
+  return sizeof(int4) + kSplitTiles * sizeof(int) + (size_t)max_row_tiles((int)M, E) * sizeof(int4) + 256;
 }
+
+// Partial sums of the split leftover tiles: one piece per workgroup at most.
+static size_t gemm_split_bytes() { return (size_t)((num_cus() + 7) & ~7) * kSplitPartBytes; }
+
+// GEMM workspace: the tile plan, then the partial-sum area.
+size_t gemm_workspace_bytes(int64_t M, int E) { return al256(gemm_plan_bytes(M, E)) + gemm_split_bytes(); }
+
+static float* split_part_in(void* ws, int M, int E) { return (float*)((char*)ws + al256(gemm_plan_bytes(M, E))); }
 
 // Kernel timing probe: one armed event pair, taken by the next forward
 // grouped-GEMM launch (single host thread).
@@ -77,18 +89,24 @@ static hipError_t probed(hipStream_t stream, F&& main) {
   return hipEventRecord(e1, stream);
 }
 
-// table_ready: `ws` already holds the tile table of these rows (a plan
-// built for kFwdTileRows-row tiles), so no tile-map launch.
-static hipError_t fwd(int epi, FwdGemm g, const int* offs, int E, int M, void* ws,
+// plan: the tile plan; part: the partial-sum area of split leftover tiles
+// (nullable: no split).  table_ready: `plan` already holds the tile table
+// of these rows (built for kFwdTileRows-row tiles), so no tile-map launch.
+static hipError_t fwd(int epi, FwdGemm g, const int* offs, int E, int M, void* plan, float* part,
                       hipStream_t stream, bool table_ready = false) {
   if (!table_ready) {
-    hipError_t err = launch_tile_map(offs, E, M, kFwdTileRows, ws, stream);
+    hipError_t err = launch_tile_map(offs, E, M, kFwdTileRows, plan, stream);
     if (err != hipSuccess) return err;
   }
-  const TileTable tt = tile_table_in(ws);
+  const TileTable tt = tile_table_in(plan);
   g.table = tt.table;
   g.n_qtiles = tt.count;
+  g.split_cnt = tt.split_cnt;
+  g.part = part;
   return probed(stream, [&] { return launch_fwd_gemm(epi, g, stream); });
+}
+static hipError_t fwd(int epi, FwdGemm g, const int* offs, int E, int M, void* ws, hipStream_t stream) {
+  return fwd(epi, g, offs, E, M, ws, split_part_in(ws, M, E), stream);
 }
 
 hipError_t launch_grouped_mm(const void* x, const void* w, const int* offs, int M, int E,
@@ -140,7 +158,7 @@ size_t moe_experts_forward_workspace_bytes(int64_t T, int64_t D, int64_t H, int 
 hipError_t launch_moe_experts_forward(const void* tokens, int T, int D, int H, int E, int K,
                                       const int* sorted_idx, const int* offs, const float* sorted_scores,
                                       bool score_before, float limit, const void* w13, const void* w2,
-                                      void* out, const void* plan, void* ws, hipStream_t stream) {
+                                      void* out, void* plan, void* ws, hipStream_t stream) {
   const int M = T * K;
   const bool permute_first = score_before || D < 128;
   auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
@@ -157,7 +175,8 @@ hipError_t launch_moe_experts_forward(const void* tokens, int T, int D, int H, i
   void* y = (K > 1) ? (void*)p : out;
   hipError_t err;
   // one tile table for both GEMMs
-  void* tp = const_cast<void*>(plan);
+  void* tp = plan;
+  float* part = split_part_in(own_plan, M, E);
   if (tp == nullptr) {
     tp = own_plan;
     if ((err = launch_tile_map(offs, E, M, kFwdTileRows, tp, stream)) != hipSuccess) return err;
@@ -168,12 +187,12 @@ hipError_t launch_moe_experts_forward(const void* tokens, int T, int D, int H, i
     if (err != hipSuccess) return err;
     FwdGemm g = {};
     g.act = routed; g.w = w13; g.kred = D; g.n = H; g.out = a; g.limit = limit;
-    err = fwd(EPI_SWIGLU, g, offs, E, M, tp, stream, true);
+    err = fwd(EPI_SWIGLU, g, offs, E, M, tp, part, stream, true);
   } else {
     FwdGemm g = {};
     g.act = tokens; g.act_index = sorted_idx; g.act_div = K; g.n_act = T;
     g.w = w13; g.kred = D; g.n = H; g.out = a; g.limit = limit;
-    err = fwd(EPI_SWIGLU, g, offs, E, M, tp, stream, true);
+    err = fwd(EPI_SWIGLU, g, offs, E, M, tp, part, stream, true);
   }
   if (err != hipSuccess) return err;
   FwdGemm g2 = {};
@@ -181,7 +200,7 @@ hipError_t launch_moe_experts_forward(const void* tokens, int T, int D, int H, i
   g2.row_scale = score_before ? nullptr : sorted_scores;
   g2.dest = sorted_idx;
   g2.n_dest = (K > 1) ? M : T;
-  if ((err = fwd(EPI_SCATTER, g2, offs, E, M, tp, stream, true)) != hipSuccess) return err;
+  if ((err = fwd(EPI_SCATTER, g2, offs, E, M, tp, part, stream, true)) != hipSuccess) return err;
   if (K > 1) return launch_combine(y, nullptr, nullptr, T, K, D, out, stream);
   return hipSuccess;
 }
@@ -255,13 +274,15 @@ hipError_t launch_grouped_mm_fp8_unpermute(const void* aq, const float* sa, cons
   return fp8(EPI_SCATTER, a, offs, E, M, ws, stream);
 }
 
-static hipError_t dgrad(int epi, DgradGemm g, const int* offs, int E, int M, void* ws,
+static hipError_t dgrad(int epi, DgradGemm g, const int* offs, int E, int M, void* plan, float* part,
                         hipStream_t stream) {
-  hipError_t err = launch_tile_map(offs, E, M, kFwdTileRows, ws, stream);
+  hipError_t err = launch_tile_map(offs, E, M, kFwdTileRows, plan, stream);
   if (err != hipSuccess) return err;
-  const TileTable tt = tile_table_in(ws);
+  const TileTable tt = tile_table_in(plan);
   g.table = tt.table;
   g.n_qtiles = tt.count;
+  g.split_cnt = tt.split_cnt;
+  g.part = part;
   return launch_dgrad_gemm(epi, g, stream);
 }
 
@@ -284,7 +305,14 @@ hipError_t launch_grouped_mm_dgrad(const void* dy, const void* w, const int* off
   // dx[m][k] = sum_n dy[m][n] w[e][n][k]
   DgradGemm g = {};
   g.dy = dy; g.w = w; g.n_red = N; g.n_out = K; g.out = dx;
-  return dgrad(EPI_STORE, g, offs, E, M, ws, stream);
+  return dgrad(EPI_STORE, g, offs, E, M, ws, split_part_in(ws, M, E), stream);
+}
+
+hipError_t launch_grouped_mm_dgrad_unsplit(const void* dy, const void* w, const int* offs, int M, int E, int N,
+                                           int K, void* dx, void* plan, hipStream_t stream) {
+  DgradGemm g = {};
+  g.dy = dy; g.w = w; g.n_red = N; g.n_out = K; g.out = dx;
+  return dgrad(EPI_STORE, g, offs, E, M, plan, nullptr, stream);
 }
 
 hipError_t launch_grouped_mm_dgrad_swiglu(const void* dy, const void* w2, const void* h,
@@ -294,7 +322,7 @@ hipError_t launch_grouped_mm_dgrad_swiglu(const void* dy, const void* w2, const 
   // g[m][p] = sum_d dy[m][d] w2[e][d][p], then the SwiGLU backward with h
   DgradGemm g = {};
   g.dy = dy; g.w = w2; g.n_red = D; g.n_out = H; g.out = dh; g.h = h; g.limit = limit; g.a_out = a_out;
-  return dgrad(EPI_SWIGLU_BWD, g, offs, E, M, ws, stream);
+  return dgrad(EPI_SWIGLU_BWD, g, offs, E, M, ws, split_part_in(ws, M, E), stream);
 }
 
 hipError_t launch_grouped_mm_wgrad(const void* dy, const void* x, const int* offs, int M, int E,

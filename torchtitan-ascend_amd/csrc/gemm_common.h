@@ -26,10 +26,14 @@ __device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 constexpr int kTileRows = 128;
 constexpr int kFwdTileRows = 320;
 
-// Workspace of a token-row GEMM: int4 header {number of tiles, ...} followed
-// by the tile table.
+// Tile plan of a token-row GEMM: int4 header {number of tiles, ...}, the
+// arrival counters of the split tail tiles (kSplitTiles ints, zeroed
+// whenever a table is built and left at zero by every GEMM that uses them),
+// then the tile table.
+constexpr int kSplitTiles = 512;
 struct TileTable {
   int* count;
+  int* split_cnt;
   int4* table;
 };
 
@@ -38,9 +42,25 @@ inline int max_row_tiles(int M, int E) { return M / kTileRows + E + 1; }
 inline TileTable tile_table_in(void* ws) {
   TileTable t;
   t.count = (int*)ws;
-  t.table = (int4*)ws + 1;
+  t.split_cnt = (int*)ws + 4;
+  t.table = (int4*)(t.split_cnt + kSplitTiles);
   return t;
 }
+
+// Tail split of the forward / dgrad GEMM: the tiles left over after the
+// last full round of the persistent walk are cut along k into pieces that
+// run on the otherwise idle CUs; each piece writes its fp32 accumulators
+// (kSplitPartBytes, register order) to the partial-sum area of the GEMM's
+// workspace, and the last piece of a tile to arrive adds them in piece
+// order and runs the epilogue.  At most kSplitMaxPieces pieces per tile,
+// each of at least kSplitMinStages k stages, and only for walks of at most
+// kSplitMaxRounds full rounds: with more, the ragged tile heights of skewed
+// routing decide the finish time more than the leftover tiles do (C4's
+// Zipf w13, 7 rounds + 32 tiles: no gain).
+constexpr size_t kSplitPartBytes = 327680;  // 8 waves x 160 fp32 x 64 lanes
+constexpr int kSplitMaxPieces = 8;
+constexpr int kSplitMinStages = 8;
+constexpr int kSplitMaxRounds = 4;
 
 // Builds the tile table with one workgroup of NT threads (every thread
 // calls it; it synchronises the workgroup).  `range(e, r0, r1)` gives the
@@ -48,12 +68,14 @@ inline TileTable tile_table_in(void* ws) {
 // tiles of at most max_rows rows, of equal height rounded up to 32 rows
 // (540 rows at max_rows = 320 give 2 tiles of 288 rather than 320 + 220);
 // tiles are numbered in expert order.  Entries past the last tile, up to
-// max_tiles, are {-1, 0, 0, 0}.  sh: NT / 64 + 1 ints of LDS.
+// max_tiles, are {-1, 0, 0, 0}.  The split-tile arrival counters are
+// zeroed.  sh: NT / 64 + 1 ints of LDS.
 template <int NT, typename Range>
 __device__ void block_tile_table(Range range, int E, int max_tiles, int max_rows, int4* __restrict__ table,
-                                 int* __restrict__ count, int* sh) {
+                                 int* __restrict__ count, int* __restrict__ split_cnt, int* sh) {
   constexpr int NW = NT / kWave;
   const int tid = threadIdx.x;
+  for (int i = tid; i < kSplitTiles; i += NT) split_cnt[i] = 0;
   const int w = tid / kWave, l = lane_id();
   int carry = 0;
   for (int e0 = 0; e0 < E; e0 += NT) {
@@ -103,6 +125,8 @@ struct FwdGemm {
   int n;
   const int4* table;
   const int* n_qtiles;
+  int* split_cnt;  // the plan's arrival counters
+  float* part;     // nullable: partial sums of split tail tiles (no split when null)
   void* out;
   float limit;
   void* h_out;
@@ -128,6 +152,11 @@ struct FwdArgs {
   int np_tiles;  // weight-row tiles per token tile
   const int4* table;
   const int* n_qtiles;
+  // tail split (null part: none); part and split_cnt adjacent (the kernel
+  // reads both with one scalar load)
+  float* part;
+  int* split_cnt;
+  int split_max;
   bf16_t* out;
   int64_t ldo;
   // EPI_SWIGLU
@@ -155,6 +184,8 @@ struct DgradGemm {
   int n_out;
   const int4* table;
   const int* n_qtiles;
+  int* split_cnt;
+  float* part;  // nullable
   void* out;  // EPI_STORE: [M][n_out]; EPI_SWIGLU_BWD: dh [M][2 n_out]
   // EPI_SWIGLU_BWD
   const void* h;  // [M][2 n_out]

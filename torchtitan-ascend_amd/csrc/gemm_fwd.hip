@@ -38,11 +38,21 @@
 //     tile's epilogue.  Within a round the 32 workgroups of one XCD take 32
 //     consecutive tiles (same expert), so the weights are shared in its L2
 //     (the SwiGLU kernels walk the token tiles in pairs, see tile_at).
+//   * Tail split: for a walk of at most four full rounds, the tiles left
+//     over after the last full round are cut along k into up to 8 pieces
+//     that run on the otherwise idle workgroups; every piece writes its fp32
+//     accumulators to the workspace and counts its arrival (agent-scope
+//     release / atomic / acquire, as the XCDs' L2s are not coherent), and
+//     the last piece to arrive streams all partials back through LDS in
+//     piece order, so the sum does not depend on arrival order, and runs the
+//     ordinary epilogue.
 //
 // Reference semantics (torchtitanturbo/models/common/npu_gmm.py):
 //   :17-18, :31, :38  torch._grouped_mm(x, w.transpose(-2, -1), offs)
 //   :32-36            optional clamp with swiglu_limit
 //   :37               npu_swiglu: silu(gate) * up, gate = first H columns
+#include <cstddef>
+#include <cstdlib>
 #include <type_traits>
 
 #include "common.h"
@@ -81,6 +91,11 @@ constexpr int META_BYTES = TQ * 8;
 constexpr int IDX_OFF = LDS_BYTES + 3 * META_BYTES;
 constexpr int IDX_BYTES = TQ * 4;
 constexpr int LDS_TOTAL = IDX_OFF + 2 * IDX_BYTES;  // 154 KB
+// Split tail tiles: whether this workgroup's piece arrived last, in the
+// stage buffers (free by then) past the ring the partial sums stream through.
+constexpr int FLAG_OFF = 8 * 16 * 1024;
+static_assert(FLAG_OFF + 16 <= LDS_BYTES, "flag inside the stage buffers");
+static_assert(kSplitPartBytes == (size_t)WAVES * NJ * NPB * 16 * 64 * 4, "partial-sum area of a piece");
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
@@ -120,7 +135,37 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   const int slot = (b & 7) * (G >> 3) + (b >> 3);
   const int nqt = sload_int(a.n_qtiles);
   const int ntiles = nqt * a.np_tiles;
-  const int nmy = slot < ntiles ? (ntiles - slot + G - 1) / G : 0;
+  // (the schedule scalars are pinned to SGPRs: divisions are expanded in
+  // VALU, and the stage advance in issue_p must stay scalar)
+  auto U = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
+  const int ksteps = U(a.kred / TK);
+  // Tail split: the walk has R full rounds of G tiles and rt tiles left
+  // over.  Unsplit, rt workgroups run one more whole tile while the others
+  // idle.  Split, each leftover tile is cut along k into np pieces of
+  // consecutive stages, piece j of leftover tile t taken by slot j * rt + t
+  // (so one XCD's slots run the same k range of neighbouring tiles), and
+  // every slot runs R whole tiles, then at most one piece.
+  const int R = U(ntiles / G);
+  const int rt = ntiles - R * G;
+  int np = 1;
+  if (a.part != nullptr && rt > 0 && rt <= kSplitTiles && R <= kSplitMaxRounds) {
+    np = max(1, min(min(G / rt, a.split_max), ksteps / kSplitMinStages));
+    // the last piece reads np partials: keep np at most sqrt(ksteps / 2),
+    // and two pieces only for long reductions
+    while (np > 1 && ksteps < 2 * np * np) --np;
+    if (np == 2 && ksteps < 64) np = 1;
+    np = U(np);
+  }
+  const bool has_piece = np > 1 && slot < rt * np;
+  const int nfull = U(np > 1 ? R : (slot < ntiles ? (ntiles - slot + G - 1) / G : 0));
+  const int nmy = nfull + (has_piece ? 1 : 0);
+  const int pc_t = has_piece ? slot % rt : 0;  // leftover tile of the piece
+  const int pc_j = has_piece ? slot / rt : 0;  // piece index
+  const int pc_k0 = U(pc_j * ksteps / np);
+  const int pc_k1 = U((pc_j + 1) * ksteps / np);
+  const int pc_L = U(R * G + pc_t);  // its walk index
+  // np, pc_j and pc_t in one register through the k loop (unpacked after it)
+  const int pc_info = U(np | (pc_j << 8) | (pc_t << 16));
   // Persistent order of the SwiGLU (w13) kernels: token tiles in pairs,
   // weight tile major inside a pair, so 32 consecutive slots (one XCD's)
   // take both token tiles of an expert with 16 weight tiles rather than one
@@ -129,7 +174,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   // with it and keep the table order).  Returns the table order's tile id
   // (qt * np_tiles + pt).
   auto tile_at = [&](int r) {
-    const int L = r * G + slot;
+    const int L = r < nfull ? r * G + slot : pc_L;
     if constexpr (EPI != EPI_SWIGLU) return L;
     const int blk = L / (2 * a.np_tiles);
     const int in_blk = L - blk * 2 * a.np_tiles;
@@ -137,8 +182,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     const int pt = in_blk / gq;
     return (2 * blk + (in_blk - pt * gq)) * a.np_tiles + pt;
   };
-  const int ksteps = a.kred / TK;
-  const int total = nmy * ksteps;
+  const int total = nfull * ksteps + (has_piece ? pc_k1 - pc_k0 : 0);
   if (total == 0) return;
 
   const uint32_t lds0 = lds_addr(smem);
@@ -227,10 +271,12 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   // (see the k loop).  issue_p sets the stage's bases, which issue_q reads.
   uint64_t d_spb = 0, d_sqb = 0;
   uint32_t d_sst = 0;
+  // issue_p is called for stages 0, 1, 2, ... in order: the (unit, k stage)
+  // of the next one is advanced here rather than divided out per call.
+  // Past the end the last stage is issued again.
+  int n_r = 0, n_ks = nfull > 0 ? 0 : pc_k0, n_kend = nfull > 0 ? ksteps : pc_k1, n_left = total;
   auto issue_p = [&](int s) {
-    const int sc = min(s, total - 1);  // past the end: re-load the last stage
-    const int r = sc / ksteps;
-    const int ks = sc - r * ksteps;
+    const int r = n_r, ks = n_ks;
     if (r != d_r) dma_tile(r);
     d_spb = d_pbase + (PT ? (uint64_t)ks * TK * a.ldp * 2 : (uint64_t)ks * ROW_BYTES);
     d_sqb = d_qbase + (uint64_t)ks * ROW_BYTES;
@@ -251,6 +297,22 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
       }
       dma16(voff, d_spb, d_sst + i * (WAVES * 1024));
     }
+    // Advance to the next stage only now: whatever sits between the stage
+    // barrier and these DMAs delays every stage (the empty asm keeps the
+    // compiler from hoisting the update above them).  Selects, no branches.
+    n_left = __builtin_amdgcn_readfirstlane(n_left);
+    n_ks = __builtin_amdgcn_readfirstlane(n_ks);
+    n_kend = __builtin_amdgcn_readfirstlane(n_kend);
+    n_r = __builtin_amdgcn_readfirstlane(n_r);
+    asm volatile("" : "+s"(n_left), "+s"(n_ks), "+s"(n_kend), "+s"(n_r));
+    const int adv = n_left > 1 ? 1 : 0;
+    n_left -= adv;
+    const int nk = n_ks + adv;
+    const bool wrap = nk == n_kend;
+    n_r += wrap ? 1 : 0;
+    const bool full = n_r < nfull;
+    n_ks = wrap ? (full ? 0 : pc_k0) : nk;
+    n_kend = wrap ? (full ? ksteps : pc_k1) : n_kend;
   };
   // Token rows past the tile's last 32-row block are never read: skip
   // their DMA (wave-uniform: instruction i moves row block WAVES * i + w).
@@ -341,7 +403,9 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
   wait_vm_barrier<0>();
 
   int s = 0;
-  auto run_tile = [&](auto njv, int r, int row0, int row1, int pt) {
+  // nks: the unit's k stages (ksteps for a whole tile); piece: the unit is
+  // a piece of a split leftover tile.
+  auto run_tile = [&](auto njv, int r, int row0, int row1, int pt, int nks, bool piece) {
     constexpr int NJV = decltype(njv)::value;
     Frag f0, f1;  // per tile: the first fragments are read at the tile's start
     read_frag(f0, s, 0, njv);
@@ -369,7 +433,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     // issues the whole next-but-one stage at its barrier, before the
     // epilogue.  Every wave runs the same barrier sequence whatever its
     // block count.
-    for (int ks = 0; ks + 1 < ksteps; ++ks, ++s) {
+    for (int ks = 0; ks + 1 < nks; ++ks, ++s) {
       if (ks > 0) issue_q();
       read_frag(f1, s, 1, njv);
       mfma(f0);
@@ -384,7 +448,7 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     }
     // Last stage of the tile: the next tile's first fragments are read at
     // the start of that tile, with its block count.
-    if (ksteps > 1) issue_q();
+    if (nks > 1) issue_q();
     read_frag(f1, s, 1, njv);
     mfma(f0);
     read_frag(f0, s, 2, njv);
@@ -395,6 +459,106 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     issue(s + 2);
     mfma(f1);
     ++s;
+
+    // ---- split leftover tile: publish this piece's sums; the last piece
+    //      to arrive adds all of them in piece order (the same order
+    //      whichever arrives last) and runs the epilogue.  The partials are
+    //      written back from this XCD's L2 (release) before the arrival is
+    //      counted, and the last piece invalidates its caches (acquire)
+    //      before it reads the others'.  The counter is reset for the next
+    //      GEMM on this plan.
+    if (__builtin_expect(piece, 0)) {  // (laid out away from the tile path)
+      // Partial sums of leftover tile pc_t: np * kSplitPartBytes bytes at
+      // part + pc_t * np * kSplitPartBytes, wave w's share (NPB * NJ blocks
+      // of 4 KB per piece) at w * np * NPB * NJ * 4 KB, laid out block-major,
+      // then piece, then the block's four 1 KB groups (lane l: 16 bytes at
+      // 16 l).  The last piece then reads one contiguous stream per wave:
+      // 1 KB chunk i is block i / (4 np), piece i / 4 % np, group i % 4.
+      // The bases are made opaque here so that no address is computed (and
+      // kept live) in the k loop.
+      constexpr uint32_t BLK = 4 * 1024;
+      // (re-read here rather than held through the k loop)
+      int info = pc_info;
+      asm volatile("" : "+s"(info));
+      const int np = info & 0xff, pc_j = (info >> 8) & 0xff, pc_t = info >> 16;
+      const int4 pc = sload_int4((const int4*)((const char*)__builtin_amdgcn_kernarg_segment_ptr() +
+                                               offsetof(FwdArgs, part)));
+      float* const part = (float*)(((uint64_t)(uint32_t)pc.y << 32) | (uint32_t)pc.x);
+      int* const split_cnt = (int*)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z);
+      uint64_t pw = (uint64_t)part + (uint64_t)pc_t * np * kSplitPartBytes + (uint64_t)w * np * (NPB * NJ * BLK);
+      asm volatile("" : "+s"(pw));
+      uint32_t loff = (uint32_t)l * 16u;
+      asm volatile("" : "+v"(loff));
+      const uint32_t bstride = (uint32_t)np * BLK;  // one block of every piece
+#pragma unroll
+      for (int pb = 0; pb < NPB; ++pb)
+#pragma unroll
+        for (int j = 0; j < NJV; ++j) {
+          const uint64_t dst = pw + (uint64_t)((pb * NJV + j) * bstride + pc_j * BLK);
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            *(float4*)(dst + (uint32_t)(g * 1024) + loff) =
+                make_float4(acc[pb][j][4 * g], acc[pb][j][4 * g + 1], acc[pb][j][4 * g + 2], acc[pb][j][4 * g + 3]);
+        }
+      wait_vm<0>();  // this wave's partial has reached L2
+      __syncthreads();
+      int* flag = (int*)(smem + FLAG_OFF);
+      if (w == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        int old = 0;
+        if (l == 0) old = __hip_atomic_fetch_add(split_cnt + pc_t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __builtin_amdgcn_readfirstlane(old);
+        if (old == np - 1) {
+          if (l == 0) __hip_atomic_store(split_cnt + pc_t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
+        if (l == 0) *flag = (old == np - 1);
+      }
+      __syncthreads();
+      if (__builtin_amdgcn_readfirstlane(*flag) == 0) return;
+      // The sum in piece order.  Each wave streams its share through a ring
+      // of 16 one-KB LDS slots (the free stage buffers) with LDS DMA, 16 KB
+      // in flight and no VGPRs held for it: chunk i goes to slot i % 16, and
+      // exactly one DMA is issued per chunk consumed (past the end: the last
+      // chunk again, into the slot just read), so "at most 15 in flight"
+      // means chunk i has landed.
+      if constexpr (NJV > 0) {
+#pragma unroll
+        for (int pb = 0; pb < NPB; ++pb)
+#pragma unroll
+          for (int j = 0; j < NJV; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[pb][j][v] = 0.f;
+        constexpr int RING = 16;
+        const int last = NPB * NJV * 4 * np - 1;
+        const uint32_t ring = lds0 + (uint32_t)w * (RING * 1024);
+        auto fetch = [&](int i) {
+          dma16(loff, pw + (uint32_t)min(i, last) * 1024u, ring + (uint32_t)(i & (RING - 1)) * 1024u);
+        };
+#pragma unroll
+        for (int i = 0; i < RING; ++i) fetch(i);
+        const char* rbase = smem + w * (RING * 1024) + 16 * l;
+        int i = 0;
+#pragma unroll
+        for (int pb = 0; pb < NPB; ++pb)
+#pragma unroll
+          for (int j = 0; j < NJV; ++j)
+            for (int q = 0; q < np; ++q) {
+#pragma unroll
+              for (int g = 0; g < 4; ++g) {
+                wait_vm<RING - 1>();
+                const float4 v = *(const float4*)(rbase + (i & (RING - 1)) * 1024);
+                acc[pb][j][4 * g] += v.x;
+                acc[pb][j][4 * g + 1] += v.y;
+                acc[pb][j][4 * g + 2] += v.z;
+                acc[pb][j][4 * g + 3] += v.w;
+                fetch(i + RING);  // after the adds: the slot's read has completed
+                ++i;
+              }
+            }
+        wait_vm<0>();
+      }
+    }
 
     // ---- epilogue: acc[pb][j][4g + i] is (token row 64j + 32wq + r32,
     //      weight row arow[pb] + 8g + 4 * half + i).  Column validity is
@@ -585,13 +749,15 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
     // 32-row blocks of the tile (at most TQ / 32), interleaved over the two
     // token-row waves: wave wq takes blocks wq, wq + 2, ...
     const int nj = min((((ti.z - ti.y + 31) >> 5) + 1 - wq) >> 1, NJ);
+    const bool piece = r >= nfull;
+    const int nks = piece ? pc_k1 - pc_k0 : ksteps;
     switch (nj) {
-      case 5: run_tile(std::integral_constant<int, 5>{}, r, ti.y, ti.z, pt); break;
-      case 4: run_tile(std::integral_constant<int, 4>{}, r, ti.y, ti.z, pt); break;
-      case 3: run_tile(std::integral_constant<int, 3>{}, r, ti.y, ti.z, pt); break;
-      case 2: run_tile(std::integral_constant<int, 2>{}, r, ti.y, ti.z, pt); break;
-      case 1: run_tile(std::integral_constant<int, 1>{}, r, ti.y, ti.z, pt); break;
-      default: run_tile(std::integral_constant<int, 0>{}, r, ti.y, ti.z, pt); break;
+      case 5: run_tile(std::integral_constant<int, 5>{}, r, ti.y, ti.z, pt, nks, piece); break;
+      case 4: run_tile(std::integral_constant<int, 4>{}, r, ti.y, ti.z, pt, nks, piece); break;
+      case 3: run_tile(std::integral_constant<int, 3>{}, r, ti.y, ti.z, pt, nks, piece); break;
+      case 2: run_tile(std::integral_constant<int, 2>{}, r, ti.y, ti.z, pt, nks, piece); break;
+      case 1: run_tile(std::integral_constant<int, 1>{}, r, ti.y, ti.z, pt, nks, piece); break;
+      default: run_tile(std::integral_constant<int, 0>{}, r, ti.y, ti.z, pt, nks, piece); break;
     }
   }
   wait_vm<0>();  // DMAs past the end have landed before the workgroup exits
@@ -614,6 +780,17 @@ hipError_t launch_fwd(FwdArgs a, hipStream_t stream) {
 }  // namespace
 
 static int g_num_cus = 0;
+
+// Pieces per split leftover tile at most (TTAMD_GEMM_SPLIT=1 turns the
+// split off, for A/B timing).
+static int split_max() {
+  static const int v = [] {
+    const char* e = getenv("TTAMD_GEMM_SPLIT");
+    const int n = e ? atoi(e) : kSplitMaxPieces;
+    return n < 1 ? 1 : (n > kSplitMaxPieces ? kSplitMaxPieces : n);
+  }();
+  return v;
+}
 
 int num_cus() {
   if (g_num_cus == 0) {
@@ -638,6 +815,9 @@ hipError_t launch_fwd_gemm(int epi, const FwdGemm& g, hipStream_t stream) {
   a.ldp = g.kred;
   a.table = g.table;
   a.n_qtiles = g.n_qtiles;
+  a.part = g.part;
+  a.split_cnt = g.split_cnt;
+  a.split_max = split_max();
   a.out = (bf16_t*)g.out;
   if (epi == EPI_SWIGLU) {
     a.p_estride = (int64_t)2 * g.n * g.kred;
@@ -679,6 +859,9 @@ hipError_t launch_dgrad_gemm(int epi, const DgradGemm& g, hipStream_t stream) {
   a.np_tiles = (g.n_out + TP - 1) / TP;
   a.table = g.table;
   a.n_qtiles = g.n_qtiles;
+  a.part = g.part;
+  a.split_cnt = g.split_cnt;
+  a.split_max = split_max();
   a.out = (bf16_t*)g.out;
   if (epi == EPI_SWIGLU_BWD) {
     a.ldo = 2 * (int64_t)g.n_out;

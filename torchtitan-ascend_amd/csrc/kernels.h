@@ -77,6 +77,7 @@ hipError_t launch_router_backward(const float* grad, const int64_t* idx, const v
 // gemm.hip
 int gemm_max_qtiles(int M, int E);
 size_t gemm_workspace_bytes(int64_t M, int E);
+size_t gemm_plan_bytes(int64_t M, int E);
 // Largest token tile of the bf16 forward / dgrad GEMMs (tile plans are built for it).
 int gemm_fwd_tile_rows();
 // The next forward grouped-GEMM launch records these events around its main
@@ -105,9 +106,12 @@ size_t moe_experts_forward_workspace_bytes(int64_t T, int64_t D, int64_t H, int 
 hipError_t launch_moe_experts_forward(const void* tokens, int T, int D, int H, int E, int K,
                                       const int* sorted_idx, const int* offs, const float* sorted_scores,
                                       bool score_before, float limit, const void* w13, const void* w2,
-                                      void* out, const void* plan, void* ws, hipStream_t stream);
+                                      void* out, void* plan, void* ws, hipStream_t stream);
 hipError_t launch_grouped_mm_dgrad(const void* dy, const void* w, const int* offs, int M, int E,
                                    int N, int K, void* dx, void* ws, hipStream_t stream);
+// The same without the tail split: plan is gemm_plan_bytes(M, E) bytes.
+hipError_t launch_grouped_mm_dgrad_unsplit(const void* dy, const void* w, const int* offs, int M, int E, int N,
+                                           int K, void* dx, void* plan, hipStream_t stream);
 hipError_t launch_grouped_mm_dgrad_swiglu(const void* dy, const void* w2, const void* h,
                                           const int* offs, int M, int E, int D, int H,
                                           float limit, void* dh, void* a_out, void* ws,

@@ -632,7 +632,7 @@ size_t router_backward_workspace_bytes(int64_t T, int E, int64_t D) {
   const int64_t P = router_pad_e(E);
   const int64_t G = router_dw_groups(T, E, D);
   return al256((size_t)T * P * 2) + al256((size_t)P * D * 2) + al256((size_t)G * router_dw_rows(E) * D * 4) +
-         al256(16) + al256((size_t)G * 4) + al256(gemm_workspace_bytes(T, 1));
+         al256(16) + al256((size_t)G * 4) + al256(gemm_plan_bytes(T, 1));
 }
 
 hipError_t launch_router_backward(const float* grad, const int64_t* idx, const void* logits, const void* x,
@@ -683,7 +683,9 @@ hipError_t launch_router_backward(const float* grad, const int64_t* idx, const v
   if ((err = hipGetLastError()) != hipSuccess) return err;
   if (dx) {
     // dx[t][d] = sum_e dlogits[t][e] w[e][d]: dgrad with the weight [1][P][D]
-    if ((err = launch_grouped_mm_dgrad(dlog, w_pad, offs1, T, 1, P, D, dx, gws, stream)) != hipSuccess) return err;
+    // (a reduction of P <= 1024 is at most 16 k stages: not worth splitting)
+    if ((err = launch_grouped_mm_dgrad_unsplit(dlog, w_pad, offs1, T, 1, P, D, dx, gws, stream)) != hipSuccess)
+      return err;
   }
   if (dw) {
     // dw_part[g][e][d] = sum over the tokens t of group g of dlogits[t][e] x[t][d]

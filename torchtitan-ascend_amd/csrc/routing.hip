@@ -156,6 +156,7 @@ struct RouteExtras {
   float* tokens_per_expert;   // fp32 [E], += counts
   int4* plan_table;           // tile table (gemm_common.h block_tile_table)
   int* plan_count;
+  int* plan_split_cnt;
   int plan_max_tiles;
   int plan_max_rows;
 };
@@ -310,7 +311,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_rank_kernel(
         r1 = sh_start[e + 1];
       };
       block_tile_table<kRouteThreads>(range, E, x.plan_max_tiles, x.plan_max_rows, x.plan_table, x.plan_count,
-                                      sh_scan);
+                                      x.plan_split_cnt, sh_scan);
     }
   }
   // Running base of (wave w, bucket b) = chunk base + counts of earlier waves.
@@ -453,6 +454,7 @@ hipError_t launch_route_from_hist(const void* labels, bool is64, int M, int E, c
     const TileTable tt = tile_table_in(plan);
     x.plan_table = tt.table;
     x.plan_count = tt.count;
+    x.plan_split_cnt = tt.split_cnt;
     x.plan_max_tiles = max_row_tiles(M, E);
     x.plan_max_rows = plan_max_rows;
   }

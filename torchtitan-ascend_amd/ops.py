@@ -268,7 +268,7 @@ def router_route(
     sorted_idx = torch.empty(M, dtype=torch.int32, device=dev)
     inverse = torch.empty(M, dtype=torch.int32, device=dev) if with_inverse else None
     sorted_scores = torch.empty(M, dtype=torch.float32, device=dev)
-    plan = _ws(lib.ttamd_gemm_workspace_bytes(M, E), dev)
+    plan = _ws(lib.ttamd_gemm_plan_bytes(M, E), dev)
     ws = _ws(lib.ttamd_router_route_workspace_bytes(T, E, D, top_k), dev)
     _lib.call(
         "ttamd_router_route", _p(x), _p(w_router), _p(expert_bias), T, E, D, top_k, funcs[score_func],
