@@ -34,10 +34,10 @@ def _grid() -> int:
 def _pieces(ntiles: int, ksteps: int) -> int:
     """Pieces per leftover tile: at most 8, G // rt, ksteps // 8 and
     sqrt(ksteps / 2), two only for 64 stages or more, none after more than
-    4 full rounds (the kernel's rule)."""
+    6 full rounds (the kernel's rule)."""
     G = _grid()
     rt = ntiles % G
-    if rt == 0 or rt > 512 or ntiles // G > 4:
+    if rt == 0 or rt > 512 or ntiles // G > 6:
         return 1
     n = max(1, min(G // rt, 8, ksteps // 8))
     while n > 1 and ksteps < 2 * n * n:

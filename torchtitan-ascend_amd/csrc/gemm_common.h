@@ -56,11 +56,12 @@ inline TileTable tile_table_in(void* ws) {
 // each of at least kSplitMinStages k stages, and only for walks of at most
 // kSplitMaxRounds full rounds: with more, the ragged tile heights of skewed
 // routing decide the finish time more than the leftover tiles do (C4's
-// Zipf w13, 7 rounds + 32 tiles: no gain).
+// Zipf w13, 7 rounds + 32 tiles: no gain; C3's shared w13, 6 rounds + 128
+// tiles of equal height: -40 us).
 constexpr size_t kSplitPartBytes = 327680;  // 8 waves x 160 fp32 x 64 lanes
 constexpr int kSplitMaxPieces = 8;
 constexpr int kSplitMinStages = 8;
-constexpr int kSplitMaxRounds = 4;
+constexpr int kSplitMaxRounds = 6;
 
 // Builds the tile table with one workgroup of NT threads (every thread
 // calls it; it synchronises the workgroup).  `range(e, r0, r1)` gives the

@@ -38,7 +38,7 @@
 //     tile's epilogue.  Within a round the 32 workgroups of one XCD take 32
 //     consecutive tiles (same expert), so the weights are shared in its L2
 //     (the SwiGLU kernels walk the token tiles in pairs, see tile_at).
-//   * Tail split: for a walk of at most four full rounds, the tiles left
+//   * Tail split: for a walk of at most six full rounds, the tiles left
 //     over after the last full round are cut along k into up to 8 pieces
 //     that run on the otherwise idle workgroups; every piece writes its fp32
 //     accumulators to the workspace and counts its arrival (agent-scope
