@@ -3,7 +3,8 @@ every replay equals the eager two-call step on the same input, bit for bit,
 with eager work and synchronisations between the replays (replays after the
 first are where wrong graph nodes would show).  Shapes
 (Llama4-debugmodel: T=2048, D=256, H=512, E=8, top-1 sigmoid, score before
-the experts) and a reduced Qwen3-30B-A3B layer (top-8 softmax + renorm).
+the experts), a reduced Qwen3-30B-A3B layer (top-8 softmax + renorm) and a
+layer whose w13 leftover tiles are split along k.
 Reference: NpuGroupedExperts.forward with its router (npu_gmm.py:100-110)."""
 from __future__ import annotations
 
@@ -21,6 +22,9 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("T,D,H,E,K,func,norm,before", [
     (2048, 256, 512, 8, 1, "sigmoid", False, True),
     (1024, 512, 256, 32, 8, "softmax", True, False),
+    # w13: 64 tiles of 32 k stages on 256 CUs, each split into 4 pieces, so
+    # the replays reuse the plan's arrival counters
+    (1024, 2048, 1024, 8, 2, "softmax", True, False),
 ])
 def test_graph_replays_equal_eager(ops, T, D, H, E, K, func, norm, before):
     G = importlib.import_module("torchtitan-ascend_amd.graph")
