@@ -99,6 +99,8 @@ static_assert(kSplitPartBytes == (size_t)WAVES * NJ * NPB * 16 * 64 * 4, "partia
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+typedef __attribute__((address_space(1))) int gint_t;
+typedef __attribute__((address_space(1))) floatx4_t gfloatx4_t;
 
 // Chunk permutation of the 512-byte reduction-major weight rows (PT): the
 // 8 rows n0..n0+3, n0+8..n0+11 one transposed read touches land on four
@@ -484,7 +486,8 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
       const int4 pc = sload_int4((const int4*)((const char*)__builtin_amdgcn_kernarg_segment_ptr() +
                                                offsetof(FwdArgs, part)));
       float* const part = (float*)(((uint64_t)(uint32_t)pc.y << 32) | (uint32_t)pc.x);
-      int* const split_cnt = (int*)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z);
+      // (global address space: global rather than flat atomics and stores)
+      gint_t* const split_cnt = (gint_t*)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z);
       uint64_t pw = (uint64_t)part + (uint64_t)pc_t * np * kSplitPartBytes + (uint64_t)w * np * (NPB * NJ * BLK);
       asm volatile("" : "+s"(pw));
       uint32_t loff = (uint32_t)l * 16u;
@@ -497,8 +500,8 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
           const uint64_t dst = pw + (uint64_t)((pb * NJV + j) * bstride + pc_j * BLK);
 #pragma unroll
           for (int g = 0; g < 4; ++g)
-            *(float4*)(dst + (uint32_t)(g * 1024) + loff) =
-                make_float4(acc[pb][j][4 * g], acc[pb][j][4 * g + 1], acc[pb][j][4 * g + 2], acc[pb][j][4 * g + 3]);
+            *(gfloatx4_t*)(dst + (uint32_t)(g * 1024) + loff) =
+                floatx4_t{acc[pb][j][4 * g], acc[pb][j][4 * g + 1], acc[pb][j][4 * g + 2], acc[pb][j][4 * g + 3]};
         }
       wait_vm<0>();  // this wave's partial has reached L2
       __syncthreads();
