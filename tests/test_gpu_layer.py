@@ -160,7 +160,10 @@ def test_c4_deepseek_shard_full_size_sampled(pkg, ops):
 
 
 @pytest.mark.parametrize("T,D,H,gated,limit", [(300, 256, 128, True, None), (1000, 512, 192, False, None),
-                                              (77, 128, 64, True, 0.4), (64, 128, 64, False, 0.0)])
+                                              (77, 128, 64, True, 0.4), (64, 128, 64, False, 0.0),
+                                              # w2: 7 x 8 tiles of 64 k stages, split into 4 pieces
+                                              # (the accumulating, gated epilogue runs once per tile)
+                                              (2048, 2048, 4096, True, None)])
 def test_shared_expert_add_vs_oracle(pkg, ops, T, D, H, gated, limit):
     """Shared expert fused into the combine (the shared w2 GEMM adds into the
     routed output in its epilogue) against the oracle's block tail."""
