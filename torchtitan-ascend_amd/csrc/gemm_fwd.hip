@@ -514,6 +514,9 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
         if (old == np - 1) {
           if (l == 0) __hip_atomic_store(split_cnt + pc_t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+          // the cache invalidation has completed before the barrier below
+          // lets the other waves load the partials
+          wait_vm<0>();
         }
         if (l == 0) *flag = (old == np - 1);
       }
