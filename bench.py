@@ -7,13 +7,15 @@ router with renormalised weights.  One step = router (gate GEMM split over D
 grouped GEMM w13 + SwiGLU with the permute gather in its loads -> grouped
 GEMM w2 + score + un-permute -> K-way sum, on inputs already resident in HBM:
 two C-ABI calls (ttamd_router_route, ttamd_moe_experts_forward), six kernel
-launches.  The per-stage breakdown runs the same kernels one op at a time.
+launches.  In every timed step the library records one event before the
+first kernel and one after each kernel (ttamd_probe_launches), so the stage
+figures, the GEMM TFLOP/s and `roofline` come from the timed steps and the
+stages add up to at most the step.
 
 Prints ONE JSON line (bench contract) with `roofline` for the dominant
-kernel (the w13 grouped GEMM, timed in every timed step by an event pair the
-library records on the kernel's stream immediately around it) and
-`cpu_baseline` (the reference op sequence restated in torch, timed on this
-host's CPU cores on a bounded sample of the workload).
+kernel (the w13 grouped GEMM) and `cpu_baseline` (the reference op sequence
+restated in torch, timed on this host's CPU cores on a bounded sample of the
+workload).
 
 Other configs (--config c1|c3|c4|c5) are for development runs; C4 and C5
 also time the expert-parallel regroup (`regroup`: the dispatcher's _permute
@@ -68,6 +70,13 @@ def parse():
     ap.add_argument("--staged", action="store_true",
                     help="time the op-at-a-time path (router, route, then each GEMM and the sum as its own call) "
                          "instead of the two fused C-ABI calls")
+    ap.add_argument("--probe", default="chain", choices=["chain", "none"],
+                    help="fused inference configs: chain = an event between consecutive kernels of every timed "
+                         "step (stage figures from the timed steps); none = bare timed steps, stage figures from "
+                         "extra untimed steps")
+    ap.add_argument("--param-dtype", default="bf16", choices=["bf16", "fp32"],
+                    help="training configs (c3): dtype of the expert weight Parameters; fp32 is the reference's "
+                         "(npu_gmm.py:63-64, cast to bf16 per call at :31 / :38), cast once per step here")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device copy (reference for the PMC byte counters) and exit")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -189,15 +198,21 @@ def main():
                 pair[1].record()
         return out
 
+    if args.param_dtype != "bf16" and not cfg["backward"]:
+        print(json.dumps({"error": "--param-dtype applies to the training configs (c3)"}))
+        sys.exit(2)
     if cfg["backward"]:
-        w13p = w13.clone().requires_grad_(True)
-        w2p = w2.clone().requires_grad_(True)
+        # expert weights as Parameters of --param-dtype (fp32: the reference's
+        # master weights, whose bf16 values are the ones the GEMMs use)
+        pdt = torch.float32 if args.param_dtype == "fp32" else torch.bfloat16
+        w13p = w13.to(pdt).requires_grad_(True)
+        w2p = w2.to(pdt).requires_grad_(True)
         dout = torch.randn(T, D, device=dev).to(torch.bfloat16)
         xg = x.clone().requires_grad_(True)
         w_router_p = w_router.clone().requires_grad_(True)
         if shared:
-            sw13.requires_grad_(True)
-            sw2.requires_grad_(True)
+            sw13 = sw13.to(pdt).requires_grad_(True)
+            sw2 = sw2.to(pdt).requires_grad_(True)
 
         def step(ev=None):
             # a training step starts from cleared gradients (zero_grad(set_to_none=True));
@@ -235,11 +250,8 @@ def main():
     torch.cuda.synchronize()
     log(f"clock settling: {settle_steps} steps; warmup: {args.warmup} steps")
     # Timed region: K steps between two synchronisations, nothing else on the
-    # stream but the roofline probe: the step's first forward grouped GEMM
-    # (w13) is timed by the library, which records an event pair on the
-    # kernel's stream immediately around that one kernel, in every timed
-    # step.  (Event records between kernels cost GPU time, ~3 us each; the
-    # per-stage breakdown is therefore taken from separate steps below.)
+    # stream but the library's kernel-timing events (recorded on the
+    # kernels' stream, below).
     graph = None
     if args.graph:
         if cfg["backward"] or fp8 or args.staged:
@@ -252,12 +264,31 @@ def main():
             graph.replay()
         torch.cuda.synchronize()
         log("captured the step as one HIP graph")
-    n_probe = args.steps if graph is None else min(args.steps, 50)
-    probes = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(n_probe)]
-    for pair in probes:
-        for e in pair:
+    # The fused bf16 inference step (c1, c2, c4) is timed with the
+    # launch-chain probe (--probe chain): one event before the step's first
+    # kernel and one after each of its kernels (router gate, top-k, rank, w13,
+    # w2, K-way sum), so every stage figure below comes from the timed steps
+    # and the stages add up to at most the step.  --probe none times the
+    # steps bare and takes the stage figures from extra, untimed fused steps
+    # with the chain.  The other modes (fp8, training, op-at-a-time, graph)
+    # time the w13 kernel alone with the GEMM probe.
+    fused = graph is None and not (fp8 or args.staged or cfg["backward"])
+    probe_mode = args.probe if fused else "gemm"
+    permute_first = cfg["score_before"] or D < 128
+    router_launches = ["route_hist", "route"] if zipf_idx is not None else ["router_gate", "router_topk", "route"]
+    expert_launches = ((["tile_map"] if zipf_idx is not None else []) + (["permute"] if permute_first else [])
+                       + ["gemm_w13_swiglu", "gemm_w2_unpermute"] + (["sum_topk"] if K > 1 else []))
+    launches = router_launches + expert_launches
+
+    def new_events(n):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+        for e in evs:
             e.record()  # creates the HIP events outside the timed region
+        return evs
+
+    n_probe = args.steps if graph is None else min(args.steps, 50)
+    chains = [new_events(len(launches) + 1) for _ in range(args.steps)] if probe_mode == "chain" else []
+    probes = [tuple(new_events(2)) for _ in range(n_probe)] if probe_mode == "gemm" else []
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
@@ -265,7 +296,10 @@ def main():
         if graph is not None:
             graph.replay()
         else:
-            ops.probe_next_gemm(*probes[i])
+            if probe_mode == "chain":
+                ops.probe_launches(chains[i])
+            elif probe_mode == "gemm":
+                ops.probe_next_gemm(*probes[i])
             step()
     end.record()
     torch.cuda.synchronize()
@@ -276,32 +310,51 @@ def main():
             step()
         torch.cuda.synchronize()
     ops.probe_next_gemm(None, None)
+    ops.probe_launches(None)
     ms = start.elapsed_time(end) / args.steps
-    kernel_us = sum(p[0].elapsed_time(p[1]) for p in probes) * 1000.0 / len(probes)
     log(f"timed {args.steps} steps: {ms:.3f} ms/step")
 
-    # Stage breakdown (not part of the timed steps): event pairs around every
-    # stage on the stream the kernels run on, averaged over extra forward
-    # passes (no-grad passes for the training configs).  The passes are
-    # queued back to back with one synchronisation at the end, so that no
-    # pass starts on an idle GPU (the first stage's start event would then
-    # also time the host's launch of that stage).
     stage_us = {}
-    n_stage = 20
-    with torch.no_grad():  # untimed: the op-at-a-time path's first calls (op registration, workspaces)
-        for _ in range(3):
-            step_forward({})
-    torch.cuda.synchronize()
-    passes = []
-    for _ in range(n_stage):
-        ev = {}
-        with torch.no_grad():
-            step_forward(ev)
-        passes.append(ev)
-    torch.cuda.synchronize()
-    for ev in passes:
-        for name, (s0, s1) in ev.items():
-            stage_us[name] = stage_us.get(name, 0.0) + s0.elapsed_time(s1) * 1000.0 / n_stage
+    if probe_mode == "none":
+        # the same fused steps, untimed, each with the chain over its kernels
+        # (queued back to back, one synchronisation at the end)
+        chains = [new_events(len(launches) + 1) for _ in range(20)]
+        torch.cuda.synchronize()
+        for c in chains:
+            ops.probe_launches(c)
+            step()
+        torch.cuda.synchronize()
+        ops.probe_launches(None)
+    if probe_mode in ("chain", "none"):
+        for j, name in enumerate(launches):
+            stage_us[name] = sum(c[j].elapsed_time(c[j + 1]) for c in chains) * 1000.0 / len(chains)
+        kernel_us = stage_us["gemm_w13_swiglu"]
+        stage_source = (f"launch-chain probe (an event between consecutive kernels) in the {args.steps} timed steps"
+                        if probe_mode == "chain" else
+                        f"launch-chain probe in {len(chains)} extra, untimed fused steps (timed steps unprobed)")
+    else:
+        kernel_us = sum(p[0].elapsed_time(p[1]) for p in probes) * 1000.0 / len(probes)
+        # Stage breakdown (not part of the timed steps): event pairs around
+        # every stage of the op-at-a-time path on the stream the kernels run
+        # on, averaged over extra forward passes (no-grad passes for the
+        # training configs), queued back to back with one synchronisation at
+        # the end, so that no pass starts on an idle GPU.
+        n_stage = 20
+        with torch.no_grad():  # untimed: the op-at-a-time path's first calls (op registration, workspaces)
+            for _ in range(3):
+                step_forward({})
+        torch.cuda.synchronize()
+        passes = []
+        for _ in range(n_stage):
+            ev = {}
+            with torch.no_grad():
+                step_forward(ev)
+            passes.append(ev)
+        torch.cuda.synchronize()
+        for ev in passes:
+            for name, (s0, s1) in ev.items():
+                stage_us[name] = stage_us.get(name, 0.0) + s0.elapsed_time(s1) * 1000.0 / n_stage
+        stage_source = f"op-at-a-time path (event pairs around each stage), {n_stage} extra forward passes"
     log(f"stages (us): {json.dumps({k: round(v, 1) for k, v in stage_us.items()})}")
 
     w13_flops = 4.0 * M * D * H
@@ -350,7 +403,8 @@ def main():
         "data": "synthetic: x~N(0,1), weights~N(0,0.02), random-init router",
         "config": {"workload": cfg["name"], "tokens": T, "dim": D, "hidden": H, "experts": E, "top_k": K,
                    "router": cfg["router"], "score_before_experts": cfg["score_before"],
-                   "backward": cfg["backward"]},
+                   "backward": cfg["backward"],
+                   **({"param_dtype": args.param_dtype} if cfg["backward"] else {})},
         "layer_tflops": round(total_flops / (ms * 1e-3) / 1e12, 1),
         "grouped_gemm_tflops": round(gemm_tflops, 1),
         "grouped_gemm_frac_of_peak": round(gemm_tflops / peak, 4),
@@ -360,6 +414,7 @@ def main():
         "permute_gbs": round(permute_gbs, 1),
         "permute_frac_of_hbm": round(permute_gbs / PEAK_HBM_GBS, 4),
         "stage_us": {k: round(v, 2) for k, v in stage_us.items()},
+        "stage_source": stage_source,
         "regroup": regroup,
         "roofline": {
             "kernel": roofline_kernel_name(cfg, fp8),

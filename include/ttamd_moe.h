@@ -142,6 +142,9 @@ int ttamd_router_backward(const float* grad_top_scores,
  *   gemm_plan (nullable, ttamd_gemm_plan_bytes(T*topk, E) bytes)
  *   receives the token-tile table of the expert-sorted rows that
  *   ttamd_moe_experts_forward can use for both grouped GEMMs.
+ *   counts and offsets may be NULL only when gemm_plan and
+ *   tokens_per_expert are both NULL (TTAMD_EINVAL otherwise): the tile
+ *   table is built from the offsets and the accumulator from the counts.
  * Same argument limits as ttamd_router_fused; workspace:
  * ttamd_router_route_workspace_bytes.  Launches: gate GEMM, score + top-k
  * + histogram, rank (the histogram scan folded in for (E + 1) *
@@ -348,12 +351,13 @@ int ttamd_grouped_mm(const void* x, const void* w, const int32_t* offs,
 
 /*
  * Fused expert up-projection: h = x @ w13[e]^T (w13 [E, 2H, D], rows 0..H-1
- * gate, H..2H-1 up), optional clamp (gate <= L, -L <= up <= L when
- * swiglu_limit > 0), a = silu(gate) * up.
+ * gate, H..2H-1 up), optional clamp (gate <= L, -L <= up <= L with
+ * L = swiglu_limit, applied for every L >= 0, including 0), a = silu(gate) * up.
  * Replaces npu_gmm.py:29-37 (cumsum, grouped_mm w13, clamp, npu_swiglu).
  * x [M, D] -> a [M, H] bf16; h_out (nullable) receives the unclamped
  * pre-activation bf16 [M, 2H] for the backward.  H % 64 == 0, D % 64 == 0.
- * swiglu_limit: NaN = no clamp (the reference's swiglu_limit=None).
+ * swiglu_limit: NaN = no clamp (the reference's swiglu_limit=None);
+ * negative values are refused.
  */
 int ttamd_grouped_mm_swiglu(const void* x, const void* w13,
                             const int32_t* offs, int64_t num_rows,
@@ -593,6 +597,18 @@ int ttamd_grouped_mm_fp8_unpermute(const void* aq, const float* sa_t,
  * NULL for both disarms.  Not thread-safe: one arming thread per process.
  */
 int ttamd_probe_next_gemm(void* start_event, void* end_event);
+
+/*
+ * Arm a chain over the next num_launches kernel launches of this process's
+ * library calls (router, route, permute / quantise, grouped GEMMs, K-way
+ * sum: every kernel the entry points launch), whatever they are:
+ * events[0] is recorded on the launch's stream before the first, and
+ * events[i + 1] after the i-th, so launch i runs between events[i] and
+ * events[i + 1] (num_launches + 1 caller-owned hipEvent_t with timing
+ * enabled).  0 <= num_launches <= 16; 0 disarms.  Independent of
+ * ttamd_probe_next_gemm (both may be armed).  Not thread-safe.
+ */
+int ttamd_probe_launches(void* const* events, int num_launches);
 
 #ifdef __cplusplus
 }

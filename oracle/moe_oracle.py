@@ -27,7 +27,8 @@ PINNED = {
     "histogram": "brute-force count; torch.bincount golden; sum == M",
     "permute / unpermute": "round trip unpermute(permute(x)) == x; torch index_select/index_add golden",
     "group_labels": "torch arange.repeat.repeat_interleave golden (npu_permute.py:68-72)",
-    "router_topk": "torch softmax/sigmoid + topk golden on tie-free inputs; explicit tie cases",
+    "router_topk": "torch softmax/sigmoid + topk golden on tie-free inputs; explicit tie cases; NaN golden "
+                   "(torch.sort stable descending, same picks as torch.topk)",
     "router_logits": "torch F.linear (fp32) rounded to bf16 golden; exact bf16 values (a missing rounding or a "
                      "transposed weight fails it)",
     "experts_forward": "torch._grouped_mm golden; per-expert index_add loop and dense einsum forms",
@@ -190,8 +191,8 @@ def router_logits(x: np.ndarray, w_router: np.ndarray) -> np.ndarray:
 def router_topk(logits: np.ndarray, top_k: int, score_func: str = "softmax", route_norm: bool = False,
                 route_scale: float = 1.0, expert_bias: np.ndarray | None = None, norm_eps: float = 1e-20):
     """Scores in fp32 (softmax over experts or sigmoid); pick the top_k by
-    score (+ expert_bias for selection only), descending, ties to the lower
-    expert id; optional renormalisation by the sum of the picked scores
+    score (+ expert_bias for selection only), descending with NaN first (as
+    torch.topk ranks it), ties to the lower expert id; optional renormalisation by the sum of the picked scores
     (model.py:762-764, UPSTREAM adds norm_eps); multiply by route_scale."""
     z = np.asarray(logits, np.float32)
     if score_func == "softmax":
@@ -204,8 +205,12 @@ def router_topk(logits: np.ndarray, top_k: int, score_func: str = "softmax", rou
         raise ValueError(score_func)
     sel = s if expert_bias is None else s + np.asarray(expert_bias, np.float32)
     T, E = s.shape
-    # lexsort: primary key -sel (descending), secondary expert id (ascending)
-    order = np.lexsort((np.broadcast_to(np.arange(E), (T, E)), -sel), axis=-1)[:, :top_k]
+    # lexsort (last key primary): NaN before every number (torch.topk ranks
+    # NaN as the largest value), then -sel (descending), then the expert id
+    # (ascending): the order of torch.sort(sel, descending=True, stable=True)
+    isnan = np.isnan(sel)
+    neg = np.where(isnan, 0.0, -sel)
+    order = np.lexsort((np.broadcast_to(np.arange(E), (T, E)), neg, ~isnan), axis=-1)[:, :top_k]
     top = np.take_along_axis(s, order, axis=-1).astype(np.float64)
     if route_norm:
         top = top / (top.sum(axis=-1, keepdims=True) + norm_eps)

@@ -119,6 +119,50 @@ def router_cases():
                   indices_bias=ib.numpy())
 
 
+def router_nan_case():
+    """Selection values with NaN (a NaN logit, a NaN expert_bias entry):
+    torch.topk ranks NaN as the largest value.  Its order among several
+    NaNs is implementation-defined, so the expected indices are
+    torch.sort(descending=True, stable=True)'s (ties to the lower expert
+    id), checked here to pick the same set as torch.topk wherever a row
+    holds at most K NaNs (only NaNs where it holds more) and the same order
+    wherever it holds at most one."""
+    g = torch.Generator().manual_seed(11)
+    T, E, K = 32, 16, 4
+    logits = torch.stack([torch.randperm(E, generator=g).float() * 0.37 - 3.0 for _ in range(T)])
+    logits = logits + 0.01 * torch.randn(T, E, generator=g)
+    nan = float("nan")
+    for t in range(8):  # one NaN logit
+        logits[t, (5 * t + 3) % E] = nan
+    for t in range(8, 12):  # two or three
+        logits[t, t % E] = nan
+        logits[t, (t + 7) % E] = nan
+        if t % 2:
+            logits[t, (t + 11) % E] = nan
+    logits[12] = nan  # the whole row
+    bias = torch.randn(E, generator=g) * 0.05
+    bias[9] = nan  # expert 9 is always picked first when biased
+    s = torch.sigmoid(logits)
+
+    def pick(sel):
+        i = torch.sort(sel, dim=-1, descending=True, stable=True).indices[:, :K]
+        it = torch.topk(sel, K, dim=-1).indices
+        for r in range(T):
+            n_nan = int(torch.isnan(sel[r]).sum())
+            if n_nan <= K:  # every NaN is picked: the same set
+                assert sorted(i[r].tolist()) == sorted(it[r].tolist()), r
+            else:  # only NaNs are picked, which ones is torch's choice
+                assert bool(torch.isnan(sel[r, it[r]]).all()), r
+            if n_nan <= 1:
+                assert i[r].tolist() == it[r].tolist(), r
+        return i
+
+    i = pick(s)
+    ib = pick(s + bias)
+    _save("router_sigmoid_k4_nan", logits=logits.numpy(), top_k=np.int64(K), scores=s.gather(1, i).numpy(),
+          indices=i.numpy(), bias=bias.numpy(), scores_bias=s.gather(1, ib).numpy(), indices_bias=ib.numpy())
+
+
 def router_gate_case():
     """F.linear of the router gate (models/qwen3_5/model.py:757), bf16 output."""
     g = torch.Generator().manual_seed(7)
@@ -319,6 +363,7 @@ if __name__ == "__main__":
     routing_cases()
     permute_cases()
     router_cases()
+    router_nan_case()
     router_gate_case()
     router_backward_cases()
     shared_expert_case()

@@ -114,6 +114,34 @@ def test_probes_reject_bad_arguments():
     assert "both events or neither" in msg
     # disarming touches no GPU state
     assert lib.ttamd_probe_next_gemm(None, None) == 0
+    msg = _err(lib.ttamd_probe_launches(None, 3))
+    assert "events is null" in msg
+    msg = _err(lib.ttamd_probe_launches(p, 17))
+    assert "num_launches" in msg
+    evs = (ctypes.c_void_p * 3)(256, None, 256)
+    msg = _err(lib.ttamd_probe_launches(evs, 2))
+    assert "events[1] is null" in msg
+    assert lib.ttamd_probe_launches(None, 0) == 0
+
+
+@pytest.mark.parametrize("null_counts, null_offsets", [(True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("want", ["plan", "tokens_per_expert"])
+def test_router_route_needs_counts_offsets_for_plan(null_counts, null_offsets, want):
+    """A tile plan or the tokens_per_expert accumulator is built from the
+    counts / offsets buffers: the call is refused on the host when either
+    is missing (nothing reaches the device)."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    T, E, D, K = 64, 8, 128, 2
+    wsb = lib.ttamd_router_route_workspace_bytes(T, E, D, K)
+    planb = lib.ttamd_gemm_plan_bytes(T * K, E)
+    counts = None if null_counts else p
+    offsets = None if null_offsets else p
+    plan = p if want == "plan" else None
+    tpe = p if want == "tokens_per_expert" else None
+    msg = _err(lib.ttamd_router_route(p, p, None, T, E, D, K, 0, 1, 0.0, 1.0, p, p, counts, offsets, p, None,
+                                      None, tpe, plan, planb, p, wsb, None))
+    assert "counts and offsets" in msg
 
 
 def test_route_noalloc_rejects_oversize_and_bad_arguments():

@@ -115,3 +115,51 @@ def test_import_has_no_side_effects():
     from conftest import ROOT
 
     subprocess.run([sys.executable, "-c", code], check=True, cwd=ROOT)
+
+
+class _FakeMesh:
+    def __init__(self, n):
+        self.n = n
+
+    def size(self):
+        return self.n
+
+
+def _dispatcher(**cfg):
+    return pkg.HipTokenDispatcher.Config(num_experts=4, top_k=1, **cfg).build()
+
+
+def test_is_local_needs_a_provable_expert_parallel_degree(monkeypatch):
+    """The single-GPU path is taken only when the expert-parallel degree is
+    provably 1; several torch.distributed ranks with nothing saying how the
+    experts are shared is an error, not a silent local run on a shard."""
+    d = _dispatcher()
+    assert d.is_local  # no process group at all
+    import torch.distributed as dist
+
+    monkeypatch.setattr(dist, "is_initialized", lambda: True)
+    monkeypatch.setattr(dist, "get_world_size", lambda *a, **k: 8)
+    with pytest.raises(RuntimeError, match="expert_parallel_degree"):
+        _ = d.is_local
+    with pytest.raises(RuntimeError, match="expert_parallel_degree"):
+        d.dispatch(torch.zeros(2, 256), torch.ones(2, 1), torch.zeros(2, 1, dtype=torch.int64))
+    # declared: data parallelism only, or a real expert-parallel degree
+    assert _dispatcher(expert_parallel_degree=1).is_local
+    d4 = _dispatcher(expert_parallel_degree=4)
+    assert not d4.is_local
+    with pytest.raises(NotImplementedError, match="expert-parallel"):
+        d4.dispatch(torch.zeros(2, 256), torch.ones(2, 1), torch.zeros(2, 1, dtype=torch.int64))
+    # an attached mesh decides, whatever its attribute name
+    for name in ("ep_mesh", "device_mesh", "process_group"):
+        d1 = _dispatcher()
+        setattr(d1, name, _FakeMesh(1))
+        assert d1.is_local
+        d2 = _dispatcher(expert_parallel_degree=1)
+        setattr(d2, name, _FakeMesh(2))
+        assert not d2.is_local
+
+
+def test_dispatcher_converter_passes_the_degree():
+    mc = _model()
+    pkg.HipTokenDispatcherConverter(pkg.HipTokenDispatcherConverter.Config(expert_parallel_degree=1)).convert(mc)
+    assert mc.layers[0].token_dispatcher.expert_parallel_degree == 1

@@ -59,22 +59,33 @@ def _spread(n_total: int, count: int, rng, tile: int = 256) -> np.ndarray:
 
 
 @pytest.mark.timeout(900)
-def test_c3_llama4_scout_fwd_bwd_full_size(pkg, ops):
+@pytest.mark.parametrize("param_dtype", ["bf16", "fp32"])
+def test_c3_llama4_scout_fwd_bwd_full_size(pkg, ops, param_dtype):
+    """param_dtype fp32: the expert weights (routed and shared) are fp32
+    nn.Parameters as in the reference (npu_gmm.py:63-64), used in bf16 by the
+    GEMMs (:31, :38: cast once per step, the forward's copy serving the
+    backward) and given fp32 gradients; the oracle sees the bf16-rounded
+    weights the reference's GEMMs see."""
     F = importlib.import_module("torchtitan-ascend_amd.functional")
     torch.manual_seed(3)
     rng = np.random.default_rng(3)
-    announce("C3 full size: set-up")
+    announce(f"C3 full size ({param_dtype} parameters): set-up")
+    wdt = torch.float32 if param_dtype == "fp32" else torch.bfloat16
     x = torch.randn(T, D, device=DEV).to(torch.bfloat16)
     w_router = (torch.randn(E, D, device=DEV) * 0.02).to(torch.bfloat16)
-    m = _build(pkg).to(DEV).to(torch.bfloat16)
+    m = _build(pkg).to(DEV).to(wdt)
     with torch.no_grad():
         m.w13.normal_(0, 0.02)
         m.w2.normal_(0, 0.02)
-    sw13 = (torch.randn(2 * H, D, device=DEV) * 0.02).to(torch.bfloat16).requires_grad_(True)
-    sw2 = (torch.randn(D, H, device=DEV) * 0.02).to(torch.bfloat16).requires_grad_(True)
+    sw13 = (torch.randn(2 * H, D, device=DEV) * 0.02).to(wdt).requires_grad_(True)
+    sw2 = (torch.randn(D, H, device=DEV) * 0.02).to(wdt).requires_grad_(True)
     dout = torch.randn(T, D, device=DEV).to(torch.bfloat16)
+    assert m.w13.dtype == wdt and m.w2.dtype == wdt
 
-    announce("C3 full size: router + layer forward + backward on the GPU")
+    def wnp(t):  # the weights as the GEMMs see them (bf16)
+        return O.bf16_round(to_np(t))
+
+    announce(f"C3 full size ({param_dtype} parameters): router + layer forward + backward on the GPU")
     # the router is part of the differentiated graph: x and w_router get its
     # gradient too (scores.grad is kept to check d(top_scores))
     xg = x.clone().requires_grad_(True)
@@ -87,6 +98,8 @@ def test_c3_llama4_scout_fwd_bwd_full_size(pkg, ops):
     out = F.shared_expert_combine(out, xg, sw13, sw2)
     out.backward(dout)
     torch.cuda.synchronize()
+    for p_ in (m.w13, m.w2, sw13, sw2):
+        assert p_.grad.dtype == wdt
 
     announce("C3 full size: oracle")
     idx_np = idx.cpu().numpy()
@@ -106,7 +119,7 @@ def test_c3_llama4_scout_fwd_bwd_full_size(pkg, ops):
     w2_all = m.w2.detach()
 
     # shared expert (one expert with every token): its part of the sampled outputs and dX
-    sw13_np, sw2_np = to_np(sw13), to_np(sw2)
+    sw13_np, sw2_np = wnp(sw13), wnp(sw2)
     ones = np.ones((tok.size, 1), np.float32)
     zeros = np.zeros((tok.size, 1), np.int64)
     sh = O.moe_backward(x_s, ones, zeros, sw13_np[None], sw2_np[None], 1, True, dout_s, round_intermediates=True)
@@ -122,7 +135,7 @@ def test_c3_llama4_scout_fwd_bwd_full_size(pkg, ops):
     for e in range(E):
         announce(f"C3 full size: oracle, expert {e}")
         sel = np.nonzero(e_tok == e)[0]
-        w13e, w2e = to_np(w13_all[e])[None], to_np(w2_all[e])[None]
+        w13e, w2e = wnp(w13_all[e])[None], wnp(w2_all[e])[None]
         if sel.size:
             z = np.zeros((sel.size, 1), np.int64)
             routed_y[sel] = O.moe_forward(x_s[sel], sc_np[tok[sel]], z, w13e, w2e, 1, True)

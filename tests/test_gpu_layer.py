@@ -93,6 +93,46 @@ def test_training_path_grads_vs_oracle(pkg, score_before, K, limit):
     assert_close(to_np(m.w2.grad), ref["dw2"], TOL, "dW2 (per expert)")
 
 
+@pytest.mark.parametrize("limit", [None, 0.5])
+def test_run_experts_grouped_mm_vs_oracle(limit):
+    """The reference-signature entry (run_experts_grouped_mm, mirroring
+    _run_experts_grouped_mm, npu_gmm.py:21-40) on its own, against the
+    oracle: fp32 x (not bf16-representable, so the .bfloat16() cast at :31
+    matters), fp32 weight Parameters (:63-64), the clamp (:32-36), empty
+    experts, the output in x's dtype (:38 type_as), and its gradients
+    (dx, dW13, dW2 in fp32; exact zeros for the experts without rows)."""
+    F = importlib.import_module("torchtitan-ascend_amd.functional")
+    rng = np.random.default_rng(61)
+    E, D, H = 8, 256, 128
+    counts = np.array([37, 0, 250, 1, 0, 128, 300, 0])
+    M = int(counts.sum())
+    x = rng.standard_normal((M, D)).astype(np.float32)
+    w13 = (rng.standard_normal((E, 2 * H, D)) * 0.05).astype(np.float32)
+    w2 = (rng.standard_normal((E, D, H)) * 0.05).astype(np.float32)
+    dout = rand_bf16(rng, (M, D))
+    xd = f32_dev(x).requires_grad_(True)
+    w13d = f32_dev(w13).requires_grad_(True)
+    w2d = f32_dev(w2).requires_grad_(True)
+    announce(f"run_experts_grouped_mm fp32 x / weights, limit={limit}")
+    y = F.run_experts_grouped_mm(w13d, w2d, xd, torch.from_numpy(counts).to(DEV), limit)
+    assert y.dtype == torch.float32 and y.shape == (M, D)
+    y.backward(f32_dev(dout))
+    xb, w13b, w2b = O.bf16_round(x), O.bf16_round(w13), O.bf16_round(w2)
+    ref_y, _, _ = O.experts_forward(xb, w13b, w2b, counts, limit)
+    assert_close(to_np(y), ref_y, TOL, "y")
+    # the same rows as a top-1 layer with unit scores applied before the
+    # experts: routed rows already in expert order, so dispatch is the identity
+    idx = np.repeat(np.arange(E), counts)[:, None].astype(np.int64)
+    ref = O.moe_backward(xb, np.ones((M, 1), np.float32), idx, w13b, w2b, E, True, dout, limit,
+                         round_intermediates=True)
+    assert xd.grad.dtype == torch.float32 and w13d.grad.dtype == torch.float32 and w2d.grad.dtype == torch.float32
+    assert_close(to_np(xd.grad), ref["dx"], TOL, "dx")
+    assert_close(to_np(w13d.grad), ref["dw13"], TOL, "dW13 (per expert)")
+    assert_close(to_np(w2d.grad), ref["dw2"], TOL, "dW2 (per expert)")
+    for e in np.nonzero(counts == 0)[0]:
+        assert not to_np(w13d.grad[e]).any() and not to_np(w2d.grad[e]).any(), f"empty expert {e}"
+
+
 def test_dispatcher_api_matches_fused_forward(pkg):
     """dispatch -> _experts_forward -> combine (the reference's call chain,
     npu_gmm.py:100-110) gives the fused path's result."""
@@ -178,7 +218,7 @@ def test_shared_expert_add_vs_oracle(pkg, ops, T, D, H, gated, limit):
     ops.shared_expert_add(out, bf16_dev(x), bf16_dev(w13), bf16_dev(w2),
                           None if gl is None else torch.from_numpy(gl).to(DEV), limit)
     ref = O.shared_expert_add(routed, x, w13, w2, gl, limit)
-    assert O.max_rel_err(to_np(out), ref) < 2e-2
+    assert_close(to_np(out), ref, 2e-2, "to_np(out)")
     # the functional form (no autograd: the fused pass) gives the same bits
     F = importlib.import_module("torchtitan-ascend_amd.functional")
     with torch.no_grad():
@@ -193,7 +233,7 @@ def test_shared_expert_add_vs_oracle(pkg, ops, T, D, H, gated, limit):
 
 
 def test_shared_expert_combine_autograd(pkg, ops):
-    """With autograd the shared expert runs as a one-expert ExpertsFn and the
+    """With autograd the shared expert runs as a one-expert ttamd::experts and the
     gate in torch; forward matches the fused pass and gradients reach x,
     both shared weights, the gate logits and the routed output."""
     rng = np.random.default_rng(3)

@@ -54,8 +54,15 @@ def _cases():
         "dispatch": (torch.ops.ttamd.dispatch, (rq(x), rq(sflat), sidx, inv, ss, K, True)),
         "dispatch_backward": (torch.ops.ttamd.dispatch_backward, (routed, x, sflat, sidx, inv, K, True)),
         "experts": (torch.ops.ttamd.experts, (rq(routed), rq(w13), rq(w2), offs, None, True)),
+        # fp32 master weights: the op returns its bf16 copies for the backward
+        "experts_fp32_weights": (torch.ops.ttamd.experts,
+                                 (rq(routed), rq(w13.float()), rq(w2.float()), offs, 0.75, True)),
         "experts_backward": (torch.ops.ttamd.experts_backward,
-                             (y, routed, h, a, w13, w2, offs, 0.75, True, True, True)),
+                             (y, routed, h, a, w13, w2, offs, 0.75, True, True, True, torch.bfloat16,
+                              torch.bfloat16)),
+        "experts_backward_fp32_grads": (torch.ops.ttamd.experts_backward,
+                                        (y, routed, h, a, w13, w2, offs, None, True, True, True, torch.float32,
+                                         torch.float32)),
         "combine": (torch.ops.ttamd.combine, (rq(y), rq(sflat), sidx, inv, K, True)),
         "combine_backward": (torch.ops.ttamd.combine_backward, (x, y, sflat, sidx, K, True, True)),
         "moe_experts_forward": (torch.ops.ttamd.moe_experts_forward, (x, sidx, offsets, ss, w13, w2, K, False, None)),
@@ -66,8 +73,8 @@ def _cases():
     }
 
 
-OP_NAMES = ["router", "router_backward", "route", "dispatch", "dispatch_backward", "experts", "experts_backward",
-            "combine", "combine_backward", "moe_experts_forward", "shared_expert_add", "token_permute",
+OP_NAMES = ["router", "router_backward", "route", "dispatch", "dispatch_backward", "experts", "experts_fp32_weights",
+            "experts_backward", "experts_backward_fp32_grads", "combine", "combine_backward", "moe_experts_forward", "shared_expert_add", "token_permute",
             "token_unpermute", "token_gather"]
 
 

@@ -1,4 +1,4 @@
-"""GPU parity of the router backward (ttamd_router_backward, RouterFn)
+"""GPU parity of the router backward (ttamd_router_backward, ttamd::router's registered backward)
 against the CPU oracle, itself pinned to torch autograd of the upstream
 router op sequence (models/qwen3_5/model.py:757-765 closed form).
 

@@ -82,6 +82,7 @@ SIGNATURES: dict[str, tuple] = {
     "ttamd_gemm_workspace_bytes": (_sz, [_i64, _i32]),
     "ttamd_gemm_plan_bytes": (_sz, [_i64, _i32]),
     "ttamd_probe_next_gemm": (_i32, [_c_void_p, _c_void_p]),
+    "ttamd_probe_launches": (_i32, [_c_void_p, _i32]),
     "ttamd_grouped_mm": (
         _i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i64, _i64, _c_void_p, _c_void_p, _sz, _c_void_p]
     ),

@@ -266,6 +266,10 @@ int ttamd_router_route(const void* x, const void* w_router, const float* expert_
           "%s: null pointer argument", fn);
   REQUIRE(w_router != nullptr, "%s: w_router is null", fn);
   REQUIRE(aligned16(x) && aligned16(w_router), "%s: x and w_router must be 16-byte aligned", fn);
+  // the tile table is built from the offsets, the accumulator from the
+  // counts (on every scan path), so both buffers must be given with them
+  REQUIRE((gemm_plan == nullptr && tokens_per_expert == nullptr) || (counts && offsets),
+          "%s: gemm_plan and tokens_per_expert need the counts and offsets buffers", fn);
   const size_t rbytes = align256(ttamd::router_workspace_bytes(num_tokens, num_experts, dim));
   TRY(check_ws(fn, workspace, workspace_bytes, ttamd_router_route_workspace_bytes(num_tokens, num_experts, dim, topk)));
   if (gemm_plan) {
@@ -509,6 +513,17 @@ int ttamd_probe_next_gemm(void* start_event, void* end_event) {
   REQUIRE((start_event == nullptr) == (end_event == nullptr),
           "ttamd_probe_next_gemm: give both events or neither");
   ttamd::gemm_probe_arm((hipEvent_t)start_event, (hipEvent_t)end_event);
+  return 0;
+}
+
+int ttamd_probe_launches(void* const* events, int num_launches) {
+  const char* fn = "ttamd_probe_launches";
+  REQUIRE(num_launches >= 0 && num_launches <= ttamd::kProbeMaxChain, "%s: num_launches must be in [0, %d]", fn,
+          ttamd::kProbeMaxChain);
+  REQUIRE(num_launches == 0 || events != nullptr, "%s: events is null", fn);
+  for (int i = 0; i <= num_launches && num_launches > 0; ++i)
+    REQUIRE(events[i] != nullptr, "%s: events[%d] is null", fn, i);
+  ttamd::probe_chain_arm((const hipEvent_t*)events, num_launches);
   return 0;
 }
 

@@ -118,14 +118,16 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 // Order-preserving unsigned key of a router selection value: a larger value
-// has a larger key, -inf the smallest of any number, NaN below it (key 1),
-// and 0 is left for a slot already picked.  -0 becomes +0 first (the two
-// compare equal).  Picking the largest key, ties to the lower expert id, is
-// the order of a stable sort of the values, descending, NaN last.
+// has a larger key, -inf the smallest of any number, NaN above +inf (the
+// largest key, whatever its sign and payload: torch.topk ranks NaN as the
+// largest value), and 0 is left for a slot already picked.  -0 becomes +0
+// first (the two compare equal).  Picking the largest key, ties to the lower
+// expert id, is the order of torch.sort(values, descending=True,
+// stable=True): NaN first, then the numbers in descending order.
 __device__ __forceinline__ uint32_t sel_key(float v) {
   const uint32_t b = __float_as_uint(v + 0.f);
   const uint32_t k = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
-  return v == v ? k : 1u;
+  return v == v ? k : 0xffffffffu;
 }
 
 __device__ __forceinline__ uint64_t lanemask_lt() {

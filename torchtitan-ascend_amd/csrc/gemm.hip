@@ -39,9 +39,11 @@ __global__ __launch_bounds__(1024) void tile_map_kernel(const int* __restrict__ 
 
 hipError_t launch_tile_map(const int* offs, int E, int M, int max_rows, void* ws, hipStream_t stream) {
   TileTable tt = tile_table_in(ws);
-  hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, stream, offs, E, M,
-                     max_row_tiles(M, E), max_rows, tt.table, tt.count, tt.split_cnt);
-  return hipGetLastError();
+  return probed(stream, false, [&] {
+    hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, stream, offs, E, M,
+                       max_row_tiles(M, E), max_rows, tt.table, tt.count, tt.split_cnt);
+    return hipGetLastError();
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -66,27 +68,21 @@ size_t gemm_workspace_bytes(int64_t M, int E) { return al256(gemm_plan_bytes(M, 
 
 static float* split_part_in(void* ws, int M, int E) { return (float*)((char*)ws + al256(gemm_plan_bytes(M, E))); }
 
-// Kernel timing probe: one armed event pair, taken by the next forward
-// grouped-GEMM launch (single host thread).
-static hipEvent_t g_probe_start = nullptr, g_probe_end = nullptr;
-
-void gemm_probe_arm(hipEvent_t start, hipEvent_t end) {
-  g_probe_start = start;
-  g_probe_end = end;
+Probe& probe() {
+  static Probe p;
+  return p;
 }
 
-// Launch `main` between the armed probe's events, if any.
-template <typename F>
-static hipError_t probed(hipStream_t stream, F&& main) {
-  hipEvent_t e0 = g_probe_start, e1 = g_probe_end;
-  g_probe_start = g_probe_end = nullptr;
-  if (e0 && e1) {
-    hipError_t err = hipEventRecord(e0, stream);
-    if (err != hipSuccess) return err;
-  }
-  hipError_t err = main();
-  if (err != hipSuccess || !(e0 && e1)) return err;
-  return hipEventRecord(e1, stream);
+void gemm_probe_arm(hipEvent_t start, hipEvent_t end) {
+  probe().gemm_start = start;
+  probe().gemm_end = end;
+}
+
+void probe_chain_arm(const hipEvent_t* events, int n_launches) {
+  Probe& p = probe();
+  p.chain_n = p.chain_i = 0;
+  for (int i = 0; i <= n_launches && n_launches > 0; ++i) p.chain[i] = events[i];
+  p.chain_n = n_launches > 0 ? n_launches : 0;
 }
 
 // plan: the tile plan; part: the partial-sum area of split leftover tiles
@@ -103,7 +99,7 @@ static hipError_t fwd(int epi, FwdGemm g, const int* offs, int E, int M, void* p
   g.n_qtiles = tt.count;
   g.split_cnt = tt.split_cnt;
   g.part = part;
-  return probed(stream, [&] { return launch_fwd_gemm(epi, g, stream); });
+  return probed(stream, true, [&] { return launch_fwd_gemm(epi, g, stream); });
 }
 static hipError_t fwd(int epi, FwdGemm g, const int* offs, int E, int M, void* ws, hipStream_t stream) {
   return fwd(epi, g, offs, E, M, ws, split_part_in(ws, M, E), stream);
@@ -213,7 +209,7 @@ static hipError_t fp8(int epi, Fp8Args a, const int* offs, int E, int M, void* w
   const TileTable tt = tile_table_in(ws);
   a.table = tt.table;
   a.n_qtiles = tt.count;
-  return probed(stream, [&] { return launch_fp8_gemm(epi, a, stream); });
+  return probed(stream, true, [&] { return launch_fp8_gemm(epi, a, stream); });
 }
 
 static Fp8Args fp8_args(const void* xq, const float* sx, const void* wq, const float* sw, int M,
@@ -283,7 +279,7 @@ static hipError_t dgrad(int epi, DgradGemm g, const int* offs, int E, int M, voi
   g.n_qtiles = tt.count;
   g.split_cnt = tt.split_cnt;
   g.part = part;
-  return launch_dgrad_gemm(epi, g, stream);
+  return probed(stream, false, [&] { return launch_dgrad_gemm(epi, g, stream); });
 }
 
 hipError_t launch_shared_expert_add(const void* x, int T, int D, int H, const void* w13s, const void* w2s,
@@ -333,7 +329,7 @@ hipError_t launch_grouped_mm_wgrad(const void* dy, const void* x, const int* off
   a.offs = offs; a.E = E; a.M = M; a.N = N; a.K = K;
   a.n_tiles = (N + 255) / 256; a.k_tiles = (K + 255) / 256;
   a.dw = dw; a.dw_fp32 = fp32 ? 1 : 0;
-  return launch_wgrad_dma(a, stream);
+  return probed(stream, false, [&] { return launch_wgrad_dma(a, stream); });
 }
 
 }  // namespace ttamd

@@ -175,6 +175,11 @@ struct FwdArgs {
   int accumulate;
   int scale_sigmoid;
 };
+// The split path of the forward kernel reads part and split_cnt with one
+// 16-byte scalar load at offsetof(FwdArgs, part).
+static_assert(offsetof(FwdArgs, split_cnt) == offsetof(FwdArgs, part) + sizeof(float*) &&
+                  offsetof(FwdArgs, part) % 8 == 0,
+              "FwdArgs: split_cnt must directly follow part");
 
 // Grouped dgrad through the forward kernel's reduction-major weight mode:
 // out[m, k] = sum_n dy[m, n] w[e(m), n, k], w [E, n_red, n_out].

@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "probe.h"
+
 namespace ttamd {
 
 // routing.hip
@@ -83,6 +85,10 @@ int gemm_fwd_tile_rows();
 // The next forward grouped-GEMM launch records these events around its main
 // kernel on its stream, then the probe disarms (nullptr, nullptr: disarm).
 void gemm_probe_arm(hipEvent_t start, hipEvent_t end);
+// The next n_launches kernel launches of the library record events[0]
+// before the first and events[i + 1] after the i-th (n_launches <=
+// kProbeMaxChain; 0 disarms).
+void probe_chain_arm(const hipEvent_t* events, int n_launches);
 hipError_t launch_grouped_mm(const void* x, const void* w, const int* offs, int M, int E, int N,
                              int K, void* out, void* ws, hipStream_t stream);
 hipError_t launch_grouped_mm_swiglu(const void* x, const void* w13, const int* offs, int M,

@@ -419,15 +419,17 @@ hipError_t launch_rank(const void* labels, bool is64, const float* scores, int M
   const size_t sh = ((size_t)(kRouteWaves + (FUSED ? 2 : 0)) * (E + 1) + (FUSED ? kRouteWaves + 1 : 0)) *
                     sizeof(int);
   const int nbits = route_nbits(E);
-  if (is64)
-    hipLaunchKernelGGL((route_rank_kernel<int64_t, FUSED>), dim3(nchunks), dim3(kRouteThreads), sh, stream,
-                       (const int64_t*)labels, scores, M, E, nbits, nchunks, hist, sorted_idx, inverse,
-                       sorted_scores, x);
-  else
-    hipLaunchKernelGGL((route_rank_kernel<int32_t, FUSED>), dim3(nchunks), dim3(kRouteThreads), sh, stream,
-                       (const int32_t*)labels, scores, M, E, nbits, nchunks, hist, sorted_idx, inverse,
-                       sorted_scores, x);
-  return hipGetLastError();
+  return probed(stream, false, [&] {
+    if (is64)
+      hipLaunchKernelGGL((route_rank_kernel<int64_t, FUSED>), dim3(nchunks), dim3(kRouteThreads), sh, stream,
+                         (const int64_t*)labels, scores, M, E, nbits, nchunks, hist, sorted_idx, inverse,
+                         sorted_scores, x);
+    else
+      hipLaunchKernelGGL((route_rank_kernel<int32_t, FUSED>), dim3(nchunks), dim3(kRouteThreads), sh, stream,
+                         (const int32_t*)labels, scores, M, E, nbits, nchunks, hist, sorted_idx, inverse,
+                         sorted_scores, x);
+    return hipGetLastError();
+  });
 }
 
 }  // namespace
@@ -459,9 +461,11 @@ hipError_t launch_route_from_hist(const void* labels, bool is64, int M, int E, c
     x.plan_max_rows = plan_max_rows;
   }
   if (M == 0) {  // nothing routed: zero counts / offsets, an empty tile table
-    hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), (size_t)(E + 2) * sizeof(int), stream,
-                       hist, 0, E, 1, 0, counts, offsets);
-    hipError_t err = hipGetLastError();
+    hipError_t err = probed(stream, false, [&] {
+      hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), (size_t)(E + 2) * sizeof(int), stream,
+                         hist, 0, E, 1, 0, counts, offsets);
+      return hipGetLastError();
+    });
     if (err == hipSuccess && plan) err = launch_tile_map(offsets + 1, E, 0, plan_max_rows, plan, stream);
     return err;
   }
@@ -470,15 +474,20 @@ hipError_t launch_route_from_hist(const void* labels, bool is64, int M, int E, c
                              stream);
   // large histograms: the single-workgroup scan, then the rank pass, the
   // tile table and the accumulation as separate launches
-  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), (size_t)(E + 2) * sizeof(int), stream,
-                     hist, (E + 1) * nchunks, E, nchunks, M, counts, offsets);
-  hipError_t err = launch_rank<false>(labels, is64, scores, M, E, nchunks, hist, sorted_idx, inverse,
+  hipError_t err = probed(stream, false, [&] {
+    hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), (size_t)(E + 2) * sizeof(int), stream,
+                       hist, (E + 1) * nchunks, E, nchunks, M, counts, offsets);
+    return hipGetLastError();
+  });
+  if (err == hipSuccess) err = launch_rank<false>(labels, is64, scores, M, E, nchunks, hist, sorted_idx, inverse,
                                       sorted_scores, RouteExtras{}, stream);
   if (err == hipSuccess && plan) err = launch_tile_map(offsets + 1, E, M, plan_max_rows, plan, stream);
   if (err == hipSuccess && tokens_per_expert) {
-    hipLaunchKernelGGL(accumulate_counts_kernel, dim3((E + 255) / 256), dim3(256), 0, stream, counts, E,
-                       tokens_per_expert);
-    err = hipGetLastError();
+    err = probed(stream, false, [&] {
+      hipLaunchKernelGGL(accumulate_counts_kernel, dim3((E + 255) / 256), dim3(256), 0, stream, counts, E,
+                         tokens_per_expert);
+      return hipGetLastError();
+    });
   }
   return err;
 }
@@ -491,13 +500,15 @@ hipError_t launch_route(const void* labels, bool is64, int M, int E,
   int* hist = (int*)ws;
   if (M > 0) {
     const size_t sh1 = (size_t)(E + 1) * sizeof(int);
-    if (is64)
-      hipLaunchKernelGGL(route_hist_kernel<int64_t>, dim3(nchunks), dim3(kRouteThreads), sh1, stream,
-                         (const int64_t*)labels, M, E, nchunks, hist);
-    else
-      hipLaunchKernelGGL(route_hist_kernel<int32_t>, dim3(nchunks), dim3(kRouteThreads), sh1, stream,
-                         (const int32_t*)labels, M, E, nchunks, hist);
-    hipError_t err = hipGetLastError();
+    hipError_t err = probed(stream, false, [&] {
+      if (is64)
+        hipLaunchKernelGGL(route_hist_kernel<int64_t>, dim3(nchunks), dim3(kRouteThreads), sh1, stream,
+                           (const int64_t*)labels, M, E, nchunks, hist);
+      else
+        hipLaunchKernelGGL(route_hist_kernel<int32_t>, dim3(nchunks), dim3(kRouteThreads), sh1, stream,
+                           (const int32_t*)labels, M, E, nchunks, hist);
+      return hipGetLastError();
+    });
     if (err != hipSuccess) return err;
   }
   return launch_route_from_hist(labels, is64, M, E, scores, counts, offsets, sorted_idx, inverse, sorted_scores,
@@ -564,10 +575,12 @@ hipError_t launch_gather_rows(const void* in, const int* src, const float* scale
   const int cpr = hidden / 8;
   if ((int64_t)rows * cpr == 0) return hipSuccess;
   const int grid = (int)std::min<int64_t>(((int64_t)rows + 3) / 4, 2048);
-  hipLaunchKernelGGL(gather_rows_kernel, dim3(grid), dim3(256), 0, stream,
-                     (const uint4*)in, src, scale, scale_by_src ? 1 : 0, n_in, n_src_max, rows,
-                     cpr, div, (uint4*)out);
-  return hipGetLastError();
+  return probed(stream, false, [&] {
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(grid), dim3(256), 0, stream,
+                       (const uint4*)in, src, scale, scale_by_src ? 1 : 0, n_in, n_src_max, rows,
+                       cpr, div, (uint4*)out);
+    return hipGetLastError();
+  });
 }
 
 // Dispatch in scatter form: one wave per token reads its row once and writes
@@ -627,9 +640,11 @@ hipError_t launch_dispatch_rows(const void* in, const int* inverse, const float*
   if ((int64_t)T * K == 0) return hipSuccess;
   const int cpr = hidden / 8;
   const int grid = (int)std::min<int64_t>(((int64_t)T + 3) / 4, 2048);
-  hipLaunchKernelGGL(dispatch_rows_kernel, dim3(grid), dim3(256), 0, stream, (const uint4*)in, inverse,
-                     scores, T, K, cpr, T * K, (uint4*)out);
-  return hipGetLastError();
+  return probed(stream, false, [&] {
+    hipLaunchKernelGGL(dispatch_rows_kernel, dim3(grid), dim3(256), 0, stream, (const uint4*)in, inverse,
+                       scores, T, K, cpr, T * K, (uint4*)out);
+    return hipGetLastError();
+  });
 }
 
 // inv[sorted[j]] = j.
@@ -704,9 +719,11 @@ hipError_t launch_combine(const void* in, const int* inverse, const float* probs
   if (total == 0) return hipSuccess;
   int64_t g = (total + kMoveThreads - 1) / kMoveThreads;
   if (g > 8192) g = 8192;
-  hipLaunchKernelGGL(combine_kernel, dim3((int)g), dim3(kMoveThreads), 0, stream,
-                     (const uint4*)in, inverse, probs, T, topk, T * topk, cpr, (uint4*)out);
-  return hipGetLastError();
+  return probed(stream, false, [&] {
+    hipLaunchKernelGGL(combine_kernel, dim3((int)g), dim3(kMoveThreads), 0, stream,
+                       (const uint4*)in, inverse, probs, T, topk, T * topk, cpr, (uint4*)out);
+    return hipGetLastError();
+  });
 }
 
 // out[o(j)] = <a[j], b[clamp(bidx[j] / bdiv)]>, o(j) = out_by_bidx ? bidx[j] : j.
@@ -804,8 +821,8 @@ hipError_t launch_group_labels(const int* counts_group, int G, int E_loc, int ro
 // ---------------------------------------------------------------------------
 // Router top-k: one wave per token.  Each lane holds ceil(E/64) scores in
 // registers; k rounds of a wave-wide argmax of the selection keys (sel_key:
-// value desc, -inf after every finite value, NaN last), ties to the lower
-// expert id.
+// NaN first, then value desc, -inf after every finite value), ties to the
+// lower expert id.
 // ---------------------------------------------------------------------------
 constexpr int kTopkMaxPerLane = 16;  // E <= 1024
 
@@ -845,8 +862,8 @@ __global__ __launch_bounds__(kMoveThreads) void router_topk_kernel(
 #pragma unroll
       for (int i = 0; i < PER_LANE; ++i) sc[i] = 1.f / (1.f + expf(-sc[i]));
     }
-    // selection keys (sel_key: value desc, -inf after every finite value,
-    // NaN last; 0 = not pickable)
+    // selection keys (sel_key: NaN first, then value desc, -inf after every
+    // finite value; 0 = not pickable)
     uint32_t key[PER_LANE];
 #pragma unroll
     for (int i = 0; i < PER_LANE; ++i) {

@@ -37,19 +37,6 @@ def _needs_grad(*tensors) -> bool:
     return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors)
 
 
-class RouterFn:
-    """Router forward with its backward (ttamd::router): (top_scores fp32
-    [T, K], selected_experts_indices int64 [T, K]); the expert ids carry no
-    gradient.  x [..., D] and w_router [E, D] in any float dtype (cast to
-    bf16 inside the graph, so their gradients come back in their dtype)."""
-
-    @staticmethod
-    def apply(x, w_router, top_k, score_func, route_norm, route_scale, expert_bias, norm_eps):
-        xb = x.reshape(-1, x.shape[-1]).to(_BF16).contiguous()
-        scores, idx, _ = _T.router(xb, w_router, top_k, score_func, route_norm, route_scale, expert_bias, norm_eps)
-        return scores, idx
-
-
 def router(
     x: torch.Tensor,
     w_router: torch.Tensor,
@@ -61,37 +48,32 @@ def router(
     norm_eps: float = 1e-20,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """UPSTREAM TokenChoiceTopKRouter forward: (top_scores fp32 [T, K],
-    selected_experts_indices int64 [T, K]).  Differentiable in x and
-    w_router (ttamd::router's registered backward)."""
-    return RouterFn.apply(x, w_router, top_k, score_func, route_norm, route_scale, expert_bias, norm_eps)
+    selected_experts_indices int64 [T, K]).  x [..., D] and w_router [E, D]
+    in any float dtype (bf16 inside the op, so their gradients come back in
+    their own dtype); differentiable in x and w_router through ttamd::router's
+    registered backward, the expert ids carry no gradient."""
+    xb = x.reshape(-1, x.shape[-1]).to(_BF16).contiguous()
+    scores, idx, _ = _T.router(xb, w_router, top_k, score_func, route_norm, route_scale, expert_bias, norm_eps)
+    return scores, idx
 
 
-class DispatchFn:
+def dispatch(x, scores_flat, sorted_indices, inverse, sorted_scores, top_k, score_before):
     """routed = gather of token rows in stable expert order (+ score before experts)."""
-
-    @staticmethod
-    def apply(x, scores_flat, sorted_indices, inverse, sorted_scores, top_k, score_before):
-        return _T.dispatch(x, scores_flat, sorted_indices, inverse, sorted_scores, top_k, score_before)
+    return _T.dispatch(x, scores_flat, sorted_indices, inverse, sorted_scores, top_k, score_before)
 
 
-class ExpertsFn:
+def experts(routed, w13, w2, offs, swiglu_limit):
     """y = (swiglu(clamp(x @ w13[e]^T))) @ w2[e]^T over ragged expert groups;
-    the pre-activation and SwiGLU output are kept only when a backward can
+    the pre-activation, the SwiGLU output and (for weights that are not bf16)
+    the forward's bf16 weight copies are kept only when a backward can
     follow."""
-
-    @staticmethod
-    def apply(routed, w13, w2, offs, swiglu_limit):
-        keep = _needs_grad(routed, w13, w2)
-        y, _, _ = _T.experts(routed, w13, w2, offs, swiglu_limit, keep)
-        return y
+    keep = _needs_grad(routed, w13, w2)
+    return _T.experts(routed, w13, w2, offs, swiglu_limit, keep)[0]
 
 
-class CombineFn:
+def combine(y, scores_flat, sorted_indices, inverse, top_k, score_after):
     """out[t] = sum_k w(t,k) * y[pos(t,k)], w = score if score after experts else 1."""
-
-    @staticmethod
-    def apply(y, scores_flat, sorted_indices, inverse, top_k, score_after):
-        return _T.combine(y, scores_flat, sorted_indices, inverse, top_k, score_after)
+    return _T.combine(y, scores_flat, sorted_indices, inverse, top_k, score_after)
 
 
 class HIPMoeTokenUnpermute:
@@ -111,16 +93,13 @@ class HIPMoeTokenUnpermute:
         return _T.token_unpermute(rows, sorted_indices).view(restore_shape)
 
 
-class TokenPermuteFn:
+def token_permute(rows, labels, num_labels):
     """permuted[j] = rows[sorted_indices[j]], sorted_indices the stable order of
     the row labels (torch_npu.npu_moe_token_permute with one label per row,
     npu_permute.py:74-76).  Rows move bit for bit in their own dtype; the
     backward scatters the gradient rows back, grad_rows[sorted_indices[j]] =
     grad_permuted[j] (ttamd::token_permute)."""
-
-    @staticmethod
-    def apply(rows, labels, num_labels):
-        return _T.token_permute(rows, labels, num_labels)
+    return _T.token_permute(rows, labels, num_labels)
 
 
 def run_experts_grouped_mm(
@@ -133,7 +112,7 @@ def run_experts_grouped_mm(
     """Same signature and result as the reference's _run_experts_grouped_mm
     (torchtitanturbo/models/common/npu_gmm.py:21-40), on the HIP kernels."""
     offs = torch.cumsum(num_tokens_per_expert, dim=0, dtype=torch.int32)
-    y = ExpertsFn.apply(x.to(_BF16).contiguous(), w13, w2, offs, swiglu_limit)
+    y = experts(x.to(_BF16).contiguous(), w13, w2, offs, swiglu_limit)
     return y.type_as(x)
 
 
@@ -158,8 +137,7 @@ def shared_expert_combine(
         return _T.shared_expert_add(routed_out, x, w13_shared, w2_shared, gate_logits, swiglu_limit)
     T = x.shape[0]
     all_rows = torch.full((1,), T, dtype=torch.int32, device=x.device)
-    y = ExpertsFn.apply(x.to(_BF16).contiguous(), w13_shared.unsqueeze(0), w2_shared.unsqueeze(0), all_rows,
-                        swiglu_limit)
+    y = experts(x.to(_BF16).contiguous(), w13_shared.unsqueeze(0), w2_shared.unsqueeze(0), all_rows, swiglu_limit)
     if gate_logits is not None:
         y = torch.sigmoid(gate_logits.to(y.dtype)).reshape(T, 1) * y
     return routed_out + y
@@ -236,9 +214,9 @@ def moe_experts_forward(
             out = ops.sum_topk(ybuf, K)
             mark("sum_topk", True)
         return out.to(x.dtype)
-    routed = DispatchFn.apply(xb, scores_flat, sorted_idx, inverse, sorted_scores, K, score_before_experts)
-    y = ExpertsFn.apply(routed, w13, w2, offs, swiglu_limit)
-    out = CombineFn.apply(y, scores_flat, sorted_idx, inverse, K, not score_before_experts)
+    routed = dispatch(xb, scores_flat, sorted_idx, inverse, sorted_scores, K, score_before_experts)
+    y = experts(routed, w13, w2, offs, swiglu_limit)
+    out = combine(y, scores_flat, sorted_idx, inverse, K, not score_before_experts)
     return out.to(x.dtype)
 
 

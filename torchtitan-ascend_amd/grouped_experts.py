@@ -19,7 +19,7 @@ from typing import Any
 import torch
 from torch import nn
 
-from .functional import ExpertsFn, moe_experts_forward, run_experts_grouped_mm
+from .functional import moe_experts_forward, run_experts_grouped_mm
 from .protocol import GroupedExperts, Module, ModelConfigConverter
 from .state_dict import upstream_to_fused
 from .token_dispatcher import HipTokenDispatcher
@@ -143,6 +143,5 @@ class HipGroupedExpertsConverter(ModelConfigConverter):
 __all__ = [
     "HipGroupedExperts",
     "HipGroupedExpertsConverter",
-    "ExpertsFn",
     "run_experts_grouped_mm",
 ]

@@ -172,31 +172,42 @@ dispatch.register_autograd(_dispatch_bwd, setup_context=_dispatch_setup)
 # ---------------------------------------------------------------------------
 @torch.library.custom_op("ttamd::experts", mutates_args=())
 def experts(routed: Tensor, w13: Tensor, w2: Tensor, offs: Tensor, swiglu_limit: Optional[float],
-            keep_activations: bool) -> tuple[Tensor, Tensor, Tensor]:
-    """(y [M, D], h [M, 2H], a [M, H]); h and a (the saved pre-activation and
-    SwiGLU output for the backward) are empty unless keep_activations."""
-    a, h = ops.grouped_mm_swiglu(routed, _bf(w13), offs, swiglu_limit, save_h=keep_activations)
-    y = ops.grouped_mm_unpermute(a, _bf(w2), offs)
-    if keep_activations:
-        return y, h, a
-    return y, _empty(routed), _empty(routed)
+            keep_activations: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(y [M, D], h [M, 2H], a [M, H], w13_bf16, w2_bf16).  h and a (the saved
+    pre-activation and SwiGLU output for the backward) are empty unless
+    keep_activations.  Weights that are not bf16 (the reference's fp32
+    nn.Parameters, npu_gmm.py:63-64, cast per call at :31 and :38) are cast
+    once here; with keep_activations the bf16 copies are returned too, so
+    the backward's GEMMs reuse them instead of casting again (empty for bf16
+    weights, which the backward reads directly)."""
+    w13b, w2b = _bf(w13), _bf(w2)
+    a, h = ops.grouped_mm_swiglu(routed, w13b, offs, swiglu_limit, save_h=keep_activations)
+    y = ops.grouped_mm_unpermute(a, w2b, offs)
+    if not keep_activations:
+        return y, _empty(routed), _empty(routed), _empty(routed), _empty(routed)
+    return (y, h, a, w13b if w13.dtype != _BF16 else _empty(routed),
+            w2b if w2.dtype != _BF16 else _empty(routed))
 
 
 @experts.register_fake
 def _(routed, w13, w2, offs, swiglu_limit, keep_activations):
     M, H, D = routed.shape[0], w13.shape[1] // 2, w2.shape[1]
     y = routed.new_empty((M, D), dtype=_BF16)
-    if keep_activations:
-        return y, routed.new_empty((M, 2 * H), dtype=_BF16), routed.new_empty((M, H), dtype=_BF16)
-    return y, routed.new_empty((0,)), routed.new_empty((0,))
+    e = lambda: routed.new_empty((0,))  # noqa: E731  (distinct tensors, as the real op returns)
+    if not keep_activations:
+        return y, e(), e(), e(), e()
+    return (y, routed.new_empty((M, 2 * H), dtype=_BF16), routed.new_empty((M, H), dtype=_BF16),
+            w13.new_empty(w13.shape, dtype=_BF16) if w13.dtype != _BF16 else e(),
+            w2.new_empty(w2.shape, dtype=_BF16) if w2.dtype != _BF16 else e())
 
 
 @torch.library.custom_op("ttamd::experts_backward", mutates_args=())
 def experts_backward(dy: Tensor, routed: Tensor, h: Tensor, a: Tensor, w13: Tensor, w2: Tensor, offs: Tensor,
                      swiglu_limit: Optional[float], need_d_routed: bool, need_dw13: bool,
-                     need_dw2: bool) -> tuple[Tensor, Tensor, Tensor]:
-    """(d_routed bf16 [M, D], dw13 like w13, dw2 like w2); a gradient not
-    asked for is an empty tensor.  fp32 weights get gradients accumulated and
+                     need_dw2: bool, w13_dtype: torch.dtype, w2_dtype: torch.dtype) -> tuple[Tensor, Tensor, Tensor]:
+    """(d_routed bf16 [M, D], dw13 in w13_dtype, dw2 in w2_dtype); a gradient
+    not asked for is an empty tensor.  w13 / w2 are the bf16 weights the
+    forward used; gradients of weights that are not bf16 are accumulated and
     written in fp32 by the wgrad kernel."""
     dy = dy.to(_BF16).contiguous()
     w13b, w2b = _bf(w13), _bf(w2)
@@ -206,39 +217,44 @@ def experts_backward(dy: Tensor, routed: Tensor, h: Tensor, a: Tensor, w13: Tens
     dw13 = _empty(w13)
     d_routed = _empty(routed)
     if need_dw2:
-        dw2 = ops.grouped_mm_wgrad(dy, a, offs, E, _F32 if w2.dtype != _BF16 else _BF16).to(w2.dtype)
+        dw2 = ops.grouped_mm_wgrad(dy, a, offs, E, _F32 if w2_dtype != _BF16 else _BF16).to(w2_dtype)
     if need_dw13:
-        dw13 = ops.grouped_mm_wgrad(dh, routed, offs, E, _F32 if w13.dtype != _BF16 else _BF16).to(w13.dtype)
+        dw13 = ops.grouped_mm_wgrad(dh, routed, offs, E, _F32 if w13_dtype != _BF16 else _BF16).to(w13_dtype)
     if need_d_routed:
         d_routed = ops.grouped_mm_dgrad(dh, w13b, offs)
     return d_routed, dw13, dw2
 
 
 @experts_backward.register_fake
-def _(dy, routed, h, a, w13, w2, offs, swiglu_limit, need_d_routed, need_dw13, need_dw2):
+def _(dy, routed, h, a, w13, w2, offs, swiglu_limit, need_d_routed, need_dw13, need_dw2, w13_dtype, w2_dtype):
     return (routed.new_empty(routed.shape if need_d_routed else (0,), dtype=_BF16),
-            w13.new_empty(w13.shape if need_dw13 else (0,)), w2.new_empty(w2.shape if need_dw2 else (0,)))
+            w13.new_empty(w13.shape if need_dw13 else (0,), dtype=w13_dtype),
+            w2.new_empty(w2.shape if need_dw2 else (0,), dtype=w2_dtype))
 
 
 def _experts_setup(ctx, inputs, output):
     routed, w13, w2, offs, limit, keep = inputs
-    _, h, a = output
-    ctx.save_for_backward(routed, h, a, w13, w2, offs)
+    _, h, a, w13b, w2b = output
+    # the backward's GEMMs read the forward's bf16 weights: its cast copies
+    # for fp32 (or other) weights, the parameters themselves when bf16
+    ctx.save_for_backward(routed, h, a, w13b if w13b.numel() else w13, w2b if w2b.numel() else w2, offs)
     ctx.limit = limit
     ctx.keep = keep
-    # h and a are outputs for the backward only: autograd must not fill
-    # zero gradients for them ([M, 2H] + [M, H] bf16 per call)
+    ctx.wdtypes = (w13.dtype, w2.dtype)
+    # h, a and the weight copies are outputs for the backward only: autograd
+    # must not fill zero gradients for them
     ctx.set_materialize_grads(False)
 
 
-def _experts_bwd(ctx, dy, _dh, _da):
+def _experts_bwd(ctx, dy, _dh, _da, _dw13b, _dw2b):
     if dy is None:
         return None, None, None, None, None, None
     routed, h, a, w13, w2, offs = ctx.saved_tensors
     if not ctx.keep:
         raise RuntimeError("ttamd::experts ran without keep_activations=True; its backward needs h and a")
     need = ctx.needs_input_grad
-    d_routed, dw13, dw2 = experts_backward(dy, routed, h, a, w13, w2, offs, ctx.limit, need[0], need[1], need[2])
+    d_routed, dw13, dw2 = experts_backward(dy, routed, h, a, w13, w2, offs, ctx.limit, need[0], need[1], need[2],
+                                           ctx.wdtypes[0], ctx.wdtypes[1])
     return (d_routed if need[0] else None, dw13 if need[1] else None, dw2 if need[2] else None, None, None, None)
 
 
