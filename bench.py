@@ -7,10 +7,10 @@ router with renormalised weights.  One step = router (gate GEMM split over D
 grouped GEMM w13 + SwiGLU with the permute gather in its loads -> grouped
 GEMM w2 + score + un-permute -> K-way sum, on inputs already resident in HBM:
 two C-ABI calls (ttamd_router_route, ttamd_moe_experts_forward), six kernel
-launches.  In every timed step the library records one event before the
-first kernel and one after each kernel (ttamd_probe_launches), so the stage
-figures, the GEMM TFLOP/s and `roofline` come from the timed steps and the
-stages add up to at most the step.
+launches.  In every timed step each kernel takes an event pair as its own
+start and end stamps (ttamd_probe_launches, stamped through the kernel's
+dispatch), so the stage figures, the GEMM TFLOP/s and `roofline` come from
+the timed steps and the stages add up to at most the step.
 
 Prints ONE JSON line (bench contract) with `roofline` for the dominant
 kernel (the w13 grouped GEMM) and `cpu_baseline` (the reference op sequence
@@ -71,9 +71,9 @@ def parse():
                     help="time the op-at-a-time path (router, route, then each GEMM and the sum as its own call) "
                          "instead of the two fused C-ABI calls")
     ap.add_argument("--probe", default="chain", choices=["chain", "none"],
-                    help="fused inference configs: chain = an event between consecutive kernels of every timed "
-                         "step (stage figures from the timed steps); none = bare timed steps, stage figures from "
-                         "extra untimed steps")
+                    help="fused inference configs: chain = every kernel of every timed step stamps its own start "
+                         "and end (stage figures from the timed steps); none = bare timed steps, stage figures "
+                         "from extra untimed steps")
     ap.add_argument("--param-dtype", default="bf16", choices=["bf16", "fp32"],
                     help="training configs (c3): dtype of the expert weight Parameters; fp32 is the reference's "
                          "(npu_gmm.py:63-64, cast to bf16 per call at :31 / :38), cast once per step here")
@@ -265,13 +265,16 @@ def main():
         torch.cuda.synchronize()
         log("captured the step as one HIP graph")
     # The fused bf16 inference step (c1, c2, c4) is timed with the
-    # launch-chain probe (--probe chain): one event before the step's first
-    # kernel and one after each of its kernels (router gate, top-k, rank, w13,
-    # w2, K-way sum), so every stage figure below comes from the timed steps
-    # and the stages add up to at most the step.  --probe none times the
-    # steps bare and takes the stage figures from extra, untimed fused steps
-    # with the chain.  The other modes (fp8, training, op-at-a-time, graph)
-    # time the w13 kernel alone with the GEMM probe.
+    # launch-chain probe (--probe chain): in timed step i one kernel of the
+    # step, kernel i mod n of its n launches (router gate, top-k, rank, w13,
+    # w2, K-way sum), takes an event pair as its own start and end stamps
+    # through its dispatch; the others run unstamped.  Every stage figure
+    # below is then the average over the timed steps that stamped it, and a
+    # step carries the cost of one stamped dispatch (a few microseconds;
+    # stamping all six costs ~35 us per step).  --probe none times the steps
+    # bare and takes the stage figures from extra, untimed fused steps with
+    # every kernel stamped.  The other modes (fp8, training, op-at-a-time,
+    # graph) time the w13 kernel alone with the GEMM probe.
     fused = graph is None and not (fp8 or args.staged or cfg["backward"])
     probe_mode = args.probe if fused else "gemm"
     permute_first = cfg["score_before"] or D < 128
@@ -279,6 +282,7 @@ def main():
     expert_launches = ((["tile_map"] if zipf_idx is not None else []) + (["permute"] if permute_first else [])
                        + ["gemm_w13_swiglu", "gemm_w2_unpermute"] + (["sum_topk"] if K > 1 else []))
     launches = router_launches + expert_launches
+    nl = len(launches)
 
     def new_events(n):
         evs = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
@@ -286,8 +290,17 @@ def main():
             e.record()  # creates the HIP events outside the timed region
         return evs
 
+    def one_stamped(pair, j):
+        evs = [None] * (2 * nl)
+        evs[2 * j], evs[2 * j + 1] = pair
+        return evs
+
     n_probe = args.steps if graph is None else min(args.steps, 50)
-    chains = [new_events(len(launches) + 1) for _ in range(args.steps)] if probe_mode == "chain" else []
+    if probe_mode == "chain" and args.steps < 2 * nl:
+        print(json.dumps({"error": f"--probe chain needs --steps >= {2 * nl} (each kernel stamped twice)"}))
+        sys.exit(2)
+    stamps = [tuple(new_events(2)) for _ in range(args.steps)] if probe_mode == "chain" else []
+    chains = [one_stamped(stamps[i], i % nl) for i in range(len(stamps))]
     probes = [tuple(new_events(2)) for _ in range(n_probe)] if probe_mode == "gemm" else []
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -315,23 +328,28 @@ def main():
     log(f"timed {args.steps} steps: {ms:.3f} ms/step")
 
     stage_us = {}
-    if probe_mode == "none":
-        # the same fused steps, untimed, each with the chain over its kernels
-        # (queued back to back, one synchronisation at the end)
-        chains = [new_events(len(launches) + 1) for _ in range(20)]
+    if probe_mode == "chain":
+        for j, name in enumerate(launches):
+            got = [stamps[i][0].elapsed_time(stamps[i][1]) for i in range(j, args.steps, nl)]
+            stage_us[name] = sum(got) * 1000.0 / len(got)
+        kernel_us = stage_us["gemm_w13_swiglu"]
+        stage_source = (f"launch-chain probe in the {args.steps} timed steps: step i stamps kernel i mod {nl} "
+                        f"(its own start / end through its dispatch), each stage averaged over its "
+                        f"{args.steps // nl}+ stamped steps")
+    elif probe_mode == "none":
+        # the same fused steps, untimed, every kernel stamped (queued back to
+        # back, one synchronisation at the end)
+        full = [new_events(2 * nl) for _ in range(20)]
         torch.cuda.synchronize()
-        for c in chains:
+        for c in full:
             ops.probe_launches(c)
             step()
         torch.cuda.synchronize()
         ops.probe_launches(None)
-    if probe_mode in ("chain", "none"):
         for j, name in enumerate(launches):
-            stage_us[name] = sum(c[j].elapsed_time(c[j + 1]) for c in chains) * 1000.0 / len(chains)
+            stage_us[name] = sum(c[2 * j].elapsed_time(c[2 * j + 1]) for c in full) * 1000.0 / len(full)
         kernel_us = stage_us["gemm_w13_swiglu"]
-        stage_source = (f"launch-chain probe (an event between consecutive kernels) in the {args.steps} timed steps"
-                        if probe_mode == "chain" else
-                        f"launch-chain probe in {len(chains)} extra, untimed fused steps (timed steps unprobed)")
+        stage_source = "launch-chain probe in 20 extra, untimed fused steps (timed steps unprobed)"
     else:
         kernel_us = sum(p[0].elapsed_time(p[1]) for p in probes) * 1000.0 / len(probes)
         # Stage breakdown (not part of the timed steps): event pairs around

@@ -588,25 +588,28 @@ int ttamd_grouped_mm_fp8_unpermute(const void* aq, const float* sa_t,
  * ------------------------------------------------------------------------ */
 
 /*
- * Arm the probe: the next forward grouped-GEMM launch of this process (any
- * ttamd_grouped_mm* or ttamd_grouped_mm_fp8* entry point, bf16 or fp8)
- * records start_event on its stream immediately before its main kernel
- * (after the tile-table kernel) and end_event immediately after it, then
- * disarms.  The events are caller-owned hipEvent_t created with timing
- * enabled (torch.cuda.Event(enable_timing=True) after one record()).
- * NULL for both disarms.  Not thread-safe: one arming thread per process.
+ * Arm the probe: the next grouped-GEMM main kernel of this process (any
+ * ttamd_grouped_mm* entry point, forward or dgrad, bf16 or fp8; not the
+ * tile-table kernel before it) takes start_event and end_event as its own
+ * start and end stamps (hipExtLaunchKernelGGL: nothing is enqueued between
+ * kernels), then the probe disarms.  The events are caller-owned
+ * hipEvent_t created with timing enabled (torch.cuda.Event(enable_timing=
+ * True) after one record()).  NULL for both disarms.  While a launch chain
+ * (ttamd_probe_launches) is armed it takes the launches first.  Not
+ * thread-safe: one arming thread per process.
  */
 int ttamd_probe_next_gemm(void* start_event, void* end_event);
 
 /*
  * Arm a chain over the next num_launches kernel launches of this process's
  * library calls (router, route, permute / quantise, grouped GEMMs, K-way
- * sum: every kernel the entry points launch), whatever they are:
- * events[0] is recorded on the launch's stream before the first, and
- * events[i + 1] after the i-th, so launch i runs between events[i] and
- * events[i + 1] (num_launches + 1 caller-owned hipEvent_t with timing
- * enabled).  0 <= num_launches <= 16; 0 disarms.  Independent of
- * ttamd_probe_next_gemm (both may be armed).  Not thread-safe.
+ * sum: every kernel the entry points launch), whatever they are: launch i
+ * takes events[2 i] and events[2 i + 1] as its start and end stamps
+ * (caller-owned hipEvent_t with timing enabled; the stamps come from the
+ * kernel's own dispatch), or runs unstamped when both are NULL, so a
+ * caller can time one chosen kernel of a sequence.  A stamped dispatch
+ * costs a few microseconds of GPU time.  0 <= num_launches <= 16; 0
+ * disarms.  Not thread-safe.
  */
 int ttamd_probe_launches(void* const* events, int num_launches);
 

@@ -118,9 +118,9 @@ def test_probes_reject_bad_arguments():
     assert "events is null" in msg
     msg = _err(lib.ttamd_probe_launches(p, 17))
     assert "num_launches" in msg
-    evs = (ctypes.c_void_p * 3)(256, None, 256)
+    evs = (ctypes.c_void_p * 4)(256, 256, None, 256)
     msg = _err(lib.ttamd_probe_launches(evs, 2))
-    assert "events[1] is null" in msg
+    assert "events[2] and events[3]" in msg
     assert lib.ttamd_probe_launches(None, 0) == 0
 
 

@@ -521,8 +521,9 @@ int ttamd_probe_launches(void* const* events, int num_launches) {
   REQUIRE(num_launches >= 0 && num_launches <= ttamd::kProbeMaxChain, "%s: num_launches must be in [0, %d]", fn,
           ttamd::kProbeMaxChain);
   REQUIRE(num_launches == 0 || events != nullptr, "%s: events is null", fn);
-  for (int i = 0; i <= num_launches && num_launches > 0; ++i)
-    REQUIRE(events[i] != nullptr, "%s: events[%d] is null", fn, i);
+  for (int i = 0; i < num_launches; ++i)
+    REQUIRE((events[2 * i] == nullptr) == (events[2 * i + 1] == nullptr),
+            "%s: events[%d] and events[%d] must both be given or both be NULL", fn, 2 * i, 2 * i + 1);
   ttamd::probe_chain_arm((const hipEvent_t*)events, num_launches);
   return 0;
 }

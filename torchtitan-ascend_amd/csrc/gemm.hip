@@ -39,11 +39,8 @@ __global__ __launch_bounds__(1024) void tile_map_kernel(const int* __restrict__ 
 
 hipError_t launch_tile_map(const int* offs, int E, int M, int max_rows, void* ws, hipStream_t stream) {
   TileTable tt = tile_table_in(ws);
-  return probed(stream, false, [&] {
-    hipLaunchKernelGGL(tile_map_kernel, dim3(1), dim3(1024), 0, stream, offs, E, M,
-                       max_row_tiles(M, E), max_rows, tt.table, tt.count, tt.split_cnt);
-    return hipGetLastError();
-  });
+  return launch_k(false, tile_map_kernel, dim3(1), dim3(1024), 0, stream, offs, E, M, max_row_tiles(M, E),
+                  max_rows, tt.table, tt.count, tt.split_cnt);
 }
 
 // ---------------------------------------------------------------------------
@@ -81,7 +78,7 @@ void gemm_probe_arm(hipEvent_t start, hipEvent_t end) {
 void probe_chain_arm(const hipEvent_t* events, int n_launches) {
   Probe& p = probe();
   p.chain_n = p.chain_i = 0;
-  for (int i = 0; i <= n_launches && n_launches > 0; ++i) p.chain[i] = events[i];
+  for (int i = 0; i < 2 * n_launches; ++i) p.chain[i] = events[i];
   p.chain_n = n_launches > 0 ? n_launches : 0;
 }
 
@@ -99,7 +96,7 @@ static hipError_t fwd(int epi, FwdGemm g, const int* offs, int E, int M, void* p
   g.n_qtiles = tt.count;
   g.split_cnt = tt.split_cnt;
   g.part = part;
-  return probed(stream, true, [&] { return launch_fwd_gemm(epi, g, stream); });
+  return launch_fwd_gemm(epi, g, stream);
 }
 static hipError_t fwd(int epi, FwdGemm g, const int* offs, int E, int M, void* ws, hipStream_t stream) {
   return fwd(epi, g, offs, E, M, ws, split_part_in(ws, M, E), stream);
@@ -209,7 +206,7 @@ static hipError_t fp8(int epi, Fp8Args a, const int* offs, int E, int M, void* w
   const TileTable tt = tile_table_in(ws);
   a.table = tt.table;
   a.n_qtiles = tt.count;
-  return probed(stream, true, [&] { return launch_fp8_gemm(epi, a, stream); });
+  return launch_fp8_gemm(epi, a, stream);
 }
 
 static Fp8Args fp8_args(const void* xq, const float* sx, const void* wq, const float* sw, int M,
@@ -279,7 +276,7 @@ static hipError_t dgrad(int epi, DgradGemm g, const int* offs, int E, int M, voi
   g.n_qtiles = tt.count;
   g.split_cnt = tt.split_cnt;
   g.part = part;
-  return probed(stream, false, [&] { return launch_dgrad_gemm(epi, g, stream); });
+  return launch_dgrad_gemm(epi, g, stream);
 }
 
 hipError_t launch_shared_expert_add(const void* x, int T, int D, int H, const void* w13s, const void* w2s,
@@ -329,7 +326,7 @@ hipError_t launch_grouped_mm_wgrad(const void* dy, const void* x, const int* off
   a.offs = offs; a.E = E; a.M = M; a.N = N; a.K = K;
   a.n_tiles = (N + 255) / 256; a.k_tiles = (K + 255) / 256;
   a.dw = dw; a.dw_fp32 = fp32 ? 1 : 0;
-  return probed(stream, false, [&] { return launch_wgrad_dma(a, stream); });
+  return launch_wgrad_dma(a, stream);
 }
 
 }  // namespace ttamd

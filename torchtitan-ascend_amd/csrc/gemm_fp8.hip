@@ -367,8 +367,7 @@ hipError_t launch_fp8(const Fp8Args& a, hipStream_t stream) {
     attr_set = true;
   }
   const int grid = (num_cus() + 7) & ~7;
-  hipLaunchKernelGGL(gg_fp8_kernel<EPI>, dim3(grid), dim3(FTHREADS), LDS_TOTAL, stream, a);
-  return hipGetLastError();
+  return launch_k(true, gg_fp8_kernel<EPI>, dim3(grid), dim3(FTHREADS), LDS_TOTAL, stream, a);
 }
 
 }  // namespace

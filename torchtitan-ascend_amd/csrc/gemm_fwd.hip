@@ -779,8 +779,7 @@ hipError_t launch_fwd(FwdArgs a, hipStream_t stream) {
     attr_set = true;
   }
   const int grid = (num_cus() + 7) & ~7;
-  hipLaunchKernelGGL((gg_fwd_kernel<EPI, PT, GATHER>), dim3(grid), dim3(FTHREADS), LDS_TOTAL, stream, a);
-  return hipGetLastError();
+  return launch_k(true, gg_fwd_kernel<EPI, PT, GATHER>, dim3(grid), dim3(FTHREADS), LDS_TOTAL, stream, a);
 }
 
 }  // namespace

@@ -337,8 +337,7 @@ hipError_t launch_wgrad_dma(const WgradDmaArgs& a, hipStream_t stream) {
     attr_set = true;
   }
   const int grid = (num_cus() + 7) & ~7;
-  hipLaunchKernelGGL(gg_wgrad_dma_kernel, dim3(grid), dim3(THREADS), LDS_TOTAL, stream, a);
-  return hipGetLastError();
+  return launch_k(false, gg_wgrad_dma_kernel, dim3(grid), dim3(THREADS), LDS_TOTAL, stream, a);
 }
 
 }  // namespace ttamd

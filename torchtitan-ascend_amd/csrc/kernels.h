@@ -85,9 +85,9 @@ int gemm_fwd_tile_rows();
 // The next forward grouped-GEMM launch records these events around its main
 // kernel on its stream, then the probe disarms (nullptr, nullptr: disarm).
 void gemm_probe_arm(hipEvent_t start, hipEvent_t end);
-// The next n_launches kernel launches of the library record events[0]
-// before the first and events[i + 1] after the i-th (n_launches <=
-// kProbeMaxChain; 0 disarms).
+// The next n_launches kernel launches of the library take the event pairs
+// (events[2 i], events[2 i + 1]) as their start and end stamps (n_launches
+// <= kProbeMaxChain; 0 disarms).
 void probe_chain_arm(const hipEvent_t* events, int n_launches);
 hipError_t launch_grouped_mm(const void* x, const void* w, const int* offs, int M, int E, int N,
                              int K, void* out, void* ws, hipStream_t stream);

@@ -1,18 +1,22 @@
-// Kernel timing probe (internal to libttamd_moe.so; a measurement aid with
-// no counterpart in the reference).
+// Kernel timing probe and the launch helper every kernel of the library
+// goes through (internal to libttamd_moe.so; the probe is a measurement aid
+// with no counterpart in the reference).
 //
-// Two ways to arm it, both from one host thread:
-//   * the next forward grouped-GEMM launch records an event pair immediately
-//     around its main kernel (gemm_start / gemm_end), then disarms;
+// A probed launch passes its event pair to hipExtLaunchKernelGGL, which
+// stamps the kernel's own start and end from its dispatch: nothing is
+// enqueued between kernels, so the timed kernels run back to back exactly
+// as unprobed ones do.  Two ways to arm it, from one host thread:
+//   * the next grouped-GEMM main kernel (forward, dgrad, fp8) takes the
+//     pair (gemm_start, gemm_end), then the probe disarms;
 //   * a chain over the next n kernel launches of the library, whatever they
-//     are: chain[0] is recorded before the first and chain[i + 1] after the
-//     i-th, so launch i runs between chain[i] and chain[i + 1] and n launches
-//     cost n + 1 event records (adjacent launches share their boundary).
-// Every launch site of the library that the probe may time goes through
-// probed(); it is one kernel launch.
+//     are: launch i takes (chain[2 i], chain[2 i + 1]).
+// While a chain is armed it takes every launch (the GEMM pair waits).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
+
+#include <cstdint>
 
 namespace ttamd {
 
@@ -20,36 +24,30 @@ constexpr int kProbeMaxChain = 16;
 
 struct Probe {
   hipEvent_t gemm_start = nullptr, gemm_end = nullptr;
-  hipEvent_t chain[kProbeMaxChain + 1] = {};
+  hipEvent_t chain[2 * kProbeMaxChain] = {};
   int chain_n = 0;  // launches the chain covers (0: disarmed)
-  int chain_i = 0;  // launches already recorded
+  int chain_i = 0;  // launches already taken
 };
 
 Probe& probe();
 
-// Launch `main` (one kernel) on `stream`, recording the armed events around
-// it; gemm: the launch is a forward grouped-GEMM main kernel.
-template <typename F>
-hipError_t probed(hipStream_t stream, bool gemm, F&& main) {
+// Launch `kernel` on `stream`; gemm: it is a grouped-GEMM main kernel.
+template <typename F, typename... Args>
+hipError_t launch_k(bool gemm, F kernel, dim3 grid, dim3 block, uint32_t shmem, hipStream_t stream,
+                    Args... args) {
   Probe& p = probe();
-  hipEvent_t g0 = nullptr, g1 = nullptr, c0 = nullptr, c1 = nullptr;
-  if (gemm && p.gemm_start && p.gemm_end) {
-    g0 = p.gemm_start;
-    g1 = p.gemm_end;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (p.chain_i < p.chain_n) {
+    e0 = p.chain[2 * p.chain_i];
+    e1 = p.chain[2 * p.chain_i + 1];
+    if (++p.chain_i == p.chain_n) p.chain_n = p.chain_i = 0;
+  } else if (gemm && p.gemm_start && p.gemm_end) {
+    e0 = p.gemm_start;
+    e1 = p.gemm_end;
     p.gemm_start = p.gemm_end = nullptr;
   }
-  if (p.chain_i < p.chain_n) {
-    c0 = p.chain_i == 0 ? p.chain[0] : nullptr;
-    c1 = p.chain[p.chain_i + 1];
-    if (++p.chain_i == p.chain_n) p.chain_n = p.chain_i = 0;
-  }
-  hipError_t err = hipSuccess;
-  if (c0 && (err = hipEventRecord(c0, stream)) != hipSuccess) return err;
-  if (g0 && (err = hipEventRecord(g0, stream)) != hipSuccess) return err;
-  if ((err = main()) != hipSuccess) return err;
-  if (g1 && (err = hipEventRecord(g1, stream)) != hipSuccess) return err;
-  if (c1 && (err = hipEventRecord(c1, stream)) != hipSuccess) return err;
-  return hipSuccess;
+  hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, e0, e1, 0, args...);
+  return hipGetLastError();
 }
 
 }  // namespace ttamd

@@ -178,11 +178,8 @@ hipError_t launch_quantize_rows(const void* in, const int* src_index, int src_di
                                 int n_in, int R, int K, void* q_out, float* scale_t, hipStream_t stream) {
   if (R == 0) return hipSuccess;
   const int grid = (R + kQRows - 1) / kQRows;
-  return probed(stream, false, [&] {
-    hipLaunchKernelGGL(quantize_rows_kernel, dim3(grid), dim3(256), 0, stream, (const uint4*)in, src_index,
-                       src_div, row_mul, n_in, R, K, (uint2*)q_out, scale_t);
-    return hipGetLastError();
-  });
+  return launch_k(false, quantize_rows_kernel, dim3(grid), dim3(256), 0, stream, (const uint4*)in, src_index,
+                  src_div, row_mul, n_in, R, K, (uint2*)q_out, scale_t);
 }
 
 hipError_t launch_quantize_blocks(const void* w, int E, int N, int K, void* q_out, float* scale,

@@ -519,10 +519,7 @@ hipError_t launch_gemm_eb(const RouterGemmArgs& a, int S, hipStream_t stream) {
     if (err != hipSuccess) return err;
     attr_set = true;
   }
-  return probed(stream, false, [&] {
-    hipLaunchKernelGGL(router_gemm_kernel<EB>, dim3((a.T + RT - 1) / RT, S), dim3(RTHREADS), lds, stream, a);
-    return hipGetLastError();
-  });
+  return launch_k(false, router_gemm_kernel<EB>, dim3((a.T + RT - 1) / RT, S), dim3(RTHREADS), lds, stream, a);
 }
 
 // Slices of D: enough gate-GEMM workgroups to give every CU one (each CU
@@ -598,16 +595,13 @@ hipError_t launch_router_hist(const void* x, const void* w, const float* bias, i
   const dim3 grid((T + 15) / 16);
   auto go = [&](auto pl) {
     constexpr int PL = decltype(pl)::value;
-    if (E == 16 * PL) hipLaunchKernelGGL((router_topk_partials_kernel<PL, true>), grid, dim3(256), 0, stream, k);
-    else hipLaunchKernelGGL((router_topk_partials_kernel<PL, false>), grid, dim3(256), 0, stream, k);
+    if (E == 16 * PL) return launch_k(false, router_topk_partials_kernel<PL, true>, grid, dim3(256), 0, stream, k);
+    return launch_k(false, router_topk_partials_kernel<PL, false>, grid, dim3(256), 0, stream, k);
   };
-  return probed(stream, false, [&] {
-    if (E <= 32) go(std::integral_constant<int, 2>{});
-    else if (E <= 64) go(std::integral_constant<int, 4>{});
-    else if (E <= 128) go(std::integral_constant<int, 8>{});
-    else go(std::integral_constant<int, 16>{});
-    return hipGetLastError();
-  });
+  if (E <= 32) return go(std::integral_constant<int, 2>{});
+  if (E <= 64) return go(std::integral_constant<int, 4>{});
+  if (E <= 128) return go(std::integral_constant<int, 8>{});
+  return go(std::integral_constant<int, 16>{});
 }
 
 static_assert(kRouterMaxE == 256, "EB = 8 covers 256 experts");

@@ -419,17 +419,13 @@ hipError_t launch_rank(const void* labels, bool is64, const float* scores, int M
   const size_t sh = ((size_t)(kRouteWaves + (FUSED ? 2 : 0)) * (E + 1) + (FUSED ? kRouteWaves + 1 : 0)) *
                     sizeof(int);
   const int nbits = route_nbits(E);
-  return probed(stream, false, [&] {
-    if (is64)
-      hipLaunchKernelGGL((route_rank_kernel<int64_t, FUSED>), dim3(nchunks), dim3(kRouteThreads), sh, stream,
-                         (const int64_t*)labels, scores, M, E, nbits, nchunks, hist, sorted_idx, inverse,
-                         sorted_scores, x);
-    else
-      hipLaunchKernelGGL((route_rank_kernel<int32_t, FUSED>), dim3(nchunks), dim3(kRouteThreads), sh, stream,
-                         (const int32_t*)labels, scores, M, E, nbits, nchunks, hist, sorted_idx, inverse,
-                         sorted_scores, x);
-    return hipGetLastError();
-  });
+  if (is64)
+    return launch_k(false, route_rank_kernel<int64_t, FUSED>, dim3(nchunks), dim3(kRouteThreads), (uint32_t)sh,
+                    stream, (const int64_t*)labels, scores, M, E, nbits, nchunks, hist, sorted_idx, inverse,
+                    sorted_scores, x);
+  return launch_k(false, route_rank_kernel<int32_t, FUSED>, dim3(nchunks), dim3(kRouteThreads), (uint32_t)sh,
+                  stream, (const int32_t*)labels, scores, M, E, nbits, nchunks, hist, sorted_idx, inverse,
+                  sorted_scores, x);
 }
 
 }  // namespace
@@ -461,11 +457,8 @@ hipError_t launch_route_from_hist(const void* labels, bool is64, int M, int E, c
     x.plan_max_rows = plan_max_rows;
   }
   if (M == 0) {  // nothing routed: zero counts / offsets, an empty tile table
-    hipError_t err = probed(stream, false, [&] {
-      hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), (size_t)(E + 2) * sizeof(int), stream,
-                         hist, 0, E, 1, 0, counts, offsets);
-      return hipGetLastError();
-    });
+    hipError_t err = launch_k(false, route_scan_kernel, dim3(1), dim3(kScanThreads),
+                              (uint32_t)((E + 2) * sizeof(int)), stream, hist, 0, E, 1, 0, counts, offsets);
     if (err == hipSuccess && plan) err = launch_tile_map(offsets + 1, E, 0, plan_max_rows, plan, stream);
     return err;
   }
@@ -474,20 +467,14 @@ hipError_t launch_route_from_hist(const void* labels, bool is64, int M, int E, c
                              stream);
   // large histograms: the single-workgroup scan, then the rank pass, the
   // tile table and the accumulation as separate launches
-  hipError_t err = probed(stream, false, [&] {
-    hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), (size_t)(E + 2) * sizeof(int), stream,
-                       hist, (E + 1) * nchunks, E, nchunks, M, counts, offsets);
-    return hipGetLastError();
-  });
+  hipError_t err = launch_k(false, route_scan_kernel, dim3(1), dim3(kScanThreads), (uint32_t)((E + 2) * sizeof(int)),
+                            stream, hist, (E + 1) * nchunks, E, nchunks, M, counts, offsets);
   if (err == hipSuccess) err = launch_rank<false>(labels, is64, scores, M, E, nchunks, hist, sorted_idx, inverse,
                                       sorted_scores, RouteExtras{}, stream);
   if (err == hipSuccess && plan) err = launch_tile_map(offsets + 1, E, M, plan_max_rows, plan, stream);
   if (err == hipSuccess && tokens_per_expert) {
-    err = probed(stream, false, [&] {
-      hipLaunchKernelGGL(accumulate_counts_kernel, dim3((E + 255) / 256), dim3(256), 0, stream, counts, E,
-                         tokens_per_expert);
-      return hipGetLastError();
-    });
+    err = launch_k(false, accumulate_counts_kernel, dim3((E + 255) / 256), dim3(256), 0, stream, counts, E,
+                   tokens_per_expert);
   }
   return err;
 }
@@ -500,15 +487,11 @@ hipError_t launch_route(const void* labels, bool is64, int M, int E,
   int* hist = (int*)ws;
   if (M > 0) {
     const size_t sh1 = (size_t)(E + 1) * sizeof(int);
-    hipError_t err = probed(stream, false, [&] {
-      if (is64)
-        hipLaunchKernelGGL(route_hist_kernel<int64_t>, dim3(nchunks), dim3(kRouteThreads), sh1, stream,
-                           (const int64_t*)labels, M, E, nchunks, hist);
-      else
-        hipLaunchKernelGGL(route_hist_kernel<int32_t>, dim3(nchunks), dim3(kRouteThreads), sh1, stream,
-                           (const int32_t*)labels, M, E, nchunks, hist);
-      return hipGetLastError();
-    });
+    hipError_t err =
+        is64 ? launch_k(false, route_hist_kernel<int64_t>, dim3(nchunks), dim3(kRouteThreads), (uint32_t)sh1, stream,
+                        (const int64_t*)labels, M, E, nchunks, hist)
+             : launch_k(false, route_hist_kernel<int32_t>, dim3(nchunks), dim3(kRouteThreads), (uint32_t)sh1, stream,
+                        (const int32_t*)labels, M, E, nchunks, hist);
     if (err != hipSuccess) return err;
   }
   return launch_route_from_hist(labels, is64, M, E, scores, counts, offsets, sorted_idx, inverse, sorted_scores,
@@ -575,12 +558,8 @@ hipError_t launch_gather_rows(const void* in, const int* src, const float* scale
   const int cpr = hidden / 8;
   if ((int64_t)rows * cpr == 0) return hipSuccess;
   const int grid = (int)std::min<int64_t>(((int64_t)rows + 3) / 4, 2048);
-  return probed(stream, false, [&] {
-    hipLaunchKernelGGL(gather_rows_kernel, dim3(grid), dim3(256), 0, stream,
-                       (const uint4*)in, src, scale, scale_by_src ? 1 : 0, n_in, n_src_max, rows,
-                       cpr, div, (uint4*)out);
-    return hipGetLastError();
-  });
+  return launch_k(false, gather_rows_kernel, dim3(grid), dim3(256), 0, stream, (const uint4*)in, src, scale,
+                  scale_by_src ? 1 : 0, n_in, n_src_max, rows, cpr, div, (uint4*)out);
 }
 
 // Dispatch in scatter form: one wave per token reads its row once and writes
@@ -640,11 +619,8 @@ hipError_t launch_dispatch_rows(const void* in, const int* inverse, const float*
   if ((int64_t)T * K == 0) return hipSuccess;
   const int cpr = hidden / 8;
   const int grid = (int)std::min<int64_t>(((int64_t)T + 3) / 4, 2048);
-  return probed(stream, false, [&] {
-    hipLaunchKernelGGL(dispatch_rows_kernel, dim3(grid), dim3(256), 0, stream, (const uint4*)in, inverse,
-                       scores, T, K, cpr, T * K, (uint4*)out);
-    return hipGetLastError();
-  });
+  return launch_k(false, dispatch_rows_kernel, dim3(grid), dim3(256), 0, stream, (const uint4*)in, inverse,
+                  scores, T, K, cpr, T * K, (uint4*)out);
 }
 
 // inv[sorted[j]] = j.
@@ -719,11 +695,8 @@ hipError_t launch_combine(const void* in, const int* inverse, const float* probs
   if (total == 0) return hipSuccess;
   int64_t g = (total + kMoveThreads - 1) / kMoveThreads;
   if (g > 8192) g = 8192;
-  return probed(stream, false, [&] {
-    hipLaunchKernelGGL(combine_kernel, dim3((int)g), dim3(kMoveThreads), 0, stream,
-                       (const uint4*)in, inverse, probs, T, topk, T * topk, cpr, (uint4*)out);
-    return hipGetLastError();
-  });
+  return launch_k(false, combine_kernel, dim3((int)g), dim3(kMoveThreads), 0, stream, (const uint4*)in, inverse,
+                  probs, T, topk, T * topk, cpr, (uint4*)out);
 }
 
 // out[o(j)] = <a[j], b[clamp(bidx[j] / bdiv)]>, o(j) = out_by_bidx ? bidx[j] : j.

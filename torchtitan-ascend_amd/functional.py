@@ -30,7 +30,7 @@ _T = torch.ops.ttamd
 
 
 def _bf16(w: torch.Tensor) -> torch.Tensor:
-    return w if w.dtype == _BF16 else w.to(_BF16)
+    return library._bf(w)
 
 
 def _needs_grad(*tensors) -> bool:

@@ -42,6 +42,9 @@ def _empty(t: Tensor) -> Tensor:
 
 
 def _bf(w: Tensor) -> Tensor:
+    """bf16 copy of a weight that is not bf16 (the per-call .bfloat16() of
+    npu_gmm.py:31, :38): torch's device cast, one streaming pass at
+    ~5.9 TB/s on MI355X."""
     return w if w.dtype == _BF16 else w.to(_BF16)
 
 

@@ -619,21 +619,24 @@ def probe_next_gemm(start: "torch.cuda.Event | None", end: "torch.cuda.Event | N
     _lib.call("ttamd_probe_next_gemm", ctypes.c_void_p(start.cuda_event), ctypes.c_void_p(end.cuda_event))
 
 
-def probe_launches(events: "list[torch.cuda.Event] | None") -> None:
+def probe_launches(events: "list[torch.cuda.Event | None] | None") -> None:
     """Arm the launch-chain probe (ttamd_probe_launches) over the next
-    len(events) - 1 kernel launches of the library's ops: events[0] is
-    recorded before the first, events[i + 1] after the i-th, on each
-    launch's stream, so events[i].elapsed_time(events[i + 1]) is launch i.
-    The events need enable_timing=True (recorded once here so that the HIP
-    events exist).  None (or a single event) disarms."""
-    if not events or len(events) < 2:
+    len(events) // 2 kernel launches of the library's ops: launch i takes
+    events[2 i] and events[2 i + 1] as its own start and end stamps, so
+    events[2 i].elapsed_time(events[2 i + 1]) is launch i's kernel time, or
+    runs unstamped when both are None.  The events need enable_timing=True
+    (recorded once here so that the HIP events exist).  None (or an empty
+    list) disarms."""
+    if not events:
         _lib.call("ttamd_probe_launches", None, 0)
         return
+    if len(events) % 2:
+        raise ValueError("probe_launches: give an even number of events (start, end per launch)")
     for e in events:
-        if not e.cuda_event:
+        if e is not None and not e.cuda_event:
             e.record()
-    arr = (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events])
-    _lib.call("ttamd_probe_launches", arr, len(events) - 1)
+    arr = (ctypes.c_void_p * len(events))(*[None if e is None else e.cuda_event for e in events])
+    _lib.call("ttamd_probe_launches", arr, len(events) // 2)
 
 
 def _offs(offs: torch.Tensor, dev: torch.device) -> torch.Tensor:
