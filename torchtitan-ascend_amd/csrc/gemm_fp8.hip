@@ -16,7 +16,7 @@
 // 128-byte line per row).
 //   * 8 waves, two per SIMD, 2 x 4: wave (wq, wp) owns token rows 128wq..
 //     and 64 weight rows (SWIGLU: 32 gate rows and the 32 matching up rows),
-//     i.e. 4 x 8 blocks of v_mfma_scale_f32_16x16x128_f8f6f4 (unit hardware
+//     i.e. 4 x 8 blocks of v_mfma_f32_16x16x128_f8f6f4 (no hardware
 //     scales): one MFMA covers a block's whole k = 128 scale block, and its
 //     partial sum goes straight into the fp32 accumulator times sx * sw, so
 //     the fp32 block scales are applied once per block as in the dequantised
@@ -44,6 +44,8 @@
 //     keeps the bounding DMA stream busy.
 //   * Persistent workgroups, XCD-aware slots, flattened (tile, stage) DMA
 //     stream and the EPI_SCATTER metadata in LDS follow gemm_fwd.hip.
+#include <type_traits>
+
 #include "common.h"
 #include "dma_asm.h"
 #include "gemm_common.h"
@@ -237,58 +239,80 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
 
-    for (int ks = 0; ks < ksteps; ++ks, ++s) {
-      // Stage s has landed (the only stage in flight) and every wave is done
-      // with stage s - 1: its buffer takes stage s + 1.  The DMA stream is
-      // the bound, so one stage ahead keeps it busy.
-      wait_vm_barrier<0>();
-      const bool more = s + 1 < total;
-      if (more) issue_p(s + 1);
-      const char* st = smem + (s % NSTAGE) * STAGE_BYTES;
-      i32x8_t fa[NPB16];
-      // A block's weight scale is one value for the whole wave (every lane
-      // reads the same LDS word): kept in SGPRs, it frees VGPRs for the
-      // accumulators and fragments.
-      float swv[NPB16];
+    // Token blocks of this wave's half that hold tile rows (rounded up to
+    // an even count): the blocks past them only hold clamped copies of the
+    // last row, whose products are never stored, so they are skipped.
+    const int hq = min(max(row1 - row0 - 128 * wq, 0), 128);
+    const int nbw = (((hq + 15) >> 4) + 1) & ~1;
+    auto kloop = [&](auto nbc) {
+      constexpr int NB = decltype(nbc)::value;
+      for (int ks = 0; ks < ksteps; ++ks, ++s) {
+        // Stage s has landed (the only stage in flight) and every wave is
+        // done with stage s - 1: its buffer takes stage s + 1.  The DMA
+        // stream is the bound, so one stage ahead keeps it busy.
+        wait_vm_barrier<0>();
+        const bool more = s + 1 < total;
+        if (more) issue_p(s + 1);
+        if constexpr (NB == 0) {
+          if (more) issue_q();
+        } else {
+          const char* st = smem + (s % NSTAGE) * STAGE_BYTES;
+          i32x8_t fa[NPB16];
+          // A block's weight scale is one value for the whole wave (every lane
+          // reads the same LDS word): kept in SGPRs, it frees VGPRs for the
+          // accumulators and fragments.
+          float swv[NPB16];
 #pragma unroll
-      for (int pb = 0; pb < NPB16; ++pb) {
-        fa[pb] = frag16(st, arow[pb]);
-        swv[pb] = __int_as_float(__builtin_amdgcn_readfirstlane(*(const int*)(st + SW_OFF + sw_lane(pb) * 4)));
-      }
-      i32x8_t fb[NBS];
-      float sxv[NBS];
-      auto read_b = [&](int jb) {
-        const int row = 128 * wq + 16 * jb;
-        fb[jb % NBS] = frag16(st + P_BYTES, row);
-        sxv[jb % NBS] = *(const float*)(st + SX_OFF + (row + r16) * 4);
-      };
-      read_b(0);
-      read_b(1);
-      float sx_prev = 0.f;
-      floatx4_t part[2][NPB16];
-      auto scale_add = [&](int jb, float sxj) {
+          for (int pb = 0; pb < NPB16; ++pb) {
+            fa[pb] = frag16(st, arow[pb]);
+            swv[pb] = __int_as_float(__builtin_amdgcn_readfirstlane(*(const int*)(st + SW_OFF + sw_lane(pb) * 4)));
+          }
+          i32x8_t fb[NBS];
+          float sxv[NBS];
+          auto read_b = [&](int jb) {
+            const int row = 128 * wq + 16 * jb;
+            fb[jb % NBS] = frag16(st + P_BYTES, row);
+            sxv[jb % NBS] = *(const float*)(st + SX_OFF + (row + r16) * 4);
+          };
+          read_b(0);
+          read_b(1);
+          float sx_prev = 0.f;
+          floatx4_t part[2][NPB16];
+          auto scale_add = [&](int jb, float sxj) {
 #pragma unroll
-        for (int pb = 0; pb < NPB16; ++pb) {
-          const float sc = swv[pb] * sxj;
+            for (int pb = 0; pb < NPB16; ++pb) {
+              const float sc = swv[pb] * sxj;
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[pb][jb][v] += part[jb & 1][pb][v] * sc;
+              for (int v = 0; v < 4; ++v) acc[pb][jb][v] += part[jb & 1][pb][v] * sc;
+            }
+          };
+#pragma unroll
+          for (int jb = 0; jb < NB; ++jb) {
+#pragma unroll
+            for (int pb = 0; pb < NPB16; ++pb) {
+              floatx4_t z = {};
+              // Zero scale operands make the compiler emit the unscaled
+              // v_mfma_f32_16x16x128_f8f6f4; the scaled form with unit E8M0
+              // scales (127) gives bit-identical sums and runs 2-3 % slower here.
+              part[jb & 1][pb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fa[pb], fb[jb % NBS], z, 0, 0, 0, 0, 0, 0);
+            }
+            // block jb - 1's scale FMAs run under block jb's MFMAs; block jb's
+            // slot then takes block jb + 2, so its row scale is kept aside first
+            if (jb > 0) scale_add(jb - 1, sx_prev);
+            sx_prev = sxv[jb % NBS];
+            if (jb + 2 < NB) read_b(jb + 2);
+            if (jb == 0 && more) issue_q();  // (later placements spill)
+          }
+          scale_add(NB - 1, sx_prev);
         }
-      };
-#pragma unroll
-      for (int jb = 0; jb < NJ16; ++jb) {
-#pragma unroll
-        for (int pb = 0; pb < NPB16; ++pb) {
-          floatx4_t z = {};
-          part[jb & 1][pb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fa[pb], fb[jb % NBS], z, 0, 0, 0, 127, 0, 127);
-        }
-        // block jb - 1's scale FMAs run under block jb's MFMAs; block jb's
-        // slot then takes block jb + 2, so its row scale is kept aside first
-        if (jb > 0) scale_add(jb - 1, sx_prev);
-        sx_prev = sxv[jb % NBS];
-        if (jb + 2 < NJ16) read_b(jb + 2);
-        if (jb == 0 && more) issue_q();  // (later placements spill)
       }
-      scale_add(NJ16 - 1, sx_prev);
+    };
+    switch (nbw) {
+      case 8: kloop(std::integral_constant<int, 8>{}); break;
+      case 6: kloop(std::integral_constant<int, 6>{}); break;
+      case 4: kloop(std::integral_constant<int, 4>{}); break;
+      case 2: kloop(std::integral_constant<int, 2>{}); break;
+      default: kloop(std::integral_constant<int, 0>{}); break;
     }
 
     // ---- epilogue: acc[pb][jb][i] is (token row 128wq + 16jb + lane % 16,
