@@ -592,6 +592,10 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
         }
       }
     };
+    // EPI_SWIGLU_BWD: the h values of block (j, pb) are loaded one block
+    // ahead, into the other half of hbuf (double buffer).
+    uint2 hbuf[2][4][2];
+    if constexpr (EPI == EPI_SWIGLU_BWD) load_h(0, 0, hbuf[0]);
 #pragma unroll
     for (int j = 0; j < NJV; ++j) {
       const int gq = row0 + 64 * j + 32 * wq + er32;
@@ -641,8 +645,9 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
         const float L = a.limit;
 #pragma unroll
         for (int pb = 0; pb < NPB; ++pb) {
-          uint2 hv[4][2];
-          load_h(j, pb, hv);
+          const int blk = j * NPB + pb;
+          if (blk + 1 < NJV * NPB) load_h((blk + 1) / NPB, (blk + 1) % NPB, hbuf[(blk + 1) & 1]);
+          const uint2 (&hv)[4][2] = hbuf[blk & 1];
           if (pt * TP + arow[pb] < a.n_p && row_ok) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
