@@ -179,6 +179,47 @@ def test_grouped_mm_fp8_unpermute_scatter_scale(ops, topk):
     assert_close(to_np(out), ref, TOL_GEMM, "to_np(out)")
 
 
+# One expert per tile height that changes the k loop's per-wave token-block
+# count (each wave computes 0, 2, 4, 6 or 8 blocks of 16 rows of its
+# 128-row half of the 256-row tile and skips the rest), plus experts split
+# into several tiles and one without rows.
+TILE_HEIGHTS = np.array([1, 16, 17, 31, 32, 33, 48, 64, 65, 96, 97, 127, 128, 129, 144, 145, 160, 161,
+                         192, 200, 224, 240, 255, 256, 0, 257, 300, 511, 513])
+
+
+@pytest.mark.parametrize("epi", ["store", "swiglu", "scatter"])
+def test_fp8_every_tile_height(ops, epi):
+    rng = np.random.default_rng(91)
+    counts = TILE_HEIGHTS
+    E, M = counts.size, int(counts.sum())
+    offs = _offs(counts)
+    announce(f"fp8 tile heights epi={epi} M={M} E={E}")
+    if epi == "store":
+        xq, sx, wq, sw, d = _quantised_operands(rng, M, E, 384, 256)
+        out = ops.grouped_mm_fp8(d["xq"], d["sx_t"], d["wq"], d["sw"], offs)
+        ref = O.grouped_mm_fp8(xq, sx, wq, sw, np.cumsum(counts))
+        assert_close(to_np(out), ref, TOL_GEMM, "fp8 store")
+    elif epi == "swiglu":
+        H = 192
+        xq, sx, wq, sw, d = _quantised_operands(rng, M, E, 2 * H, 256)
+        a, h = ops.grouped_mm_fp8_swiglu(d["xq"], d["sx_t"], d["wq"], d["sw"], offs, None, save_h=True)
+        href = O.bf16_round(O.grouped_mm_fp8(xq, sx, wq, sw, np.cumsum(counts)))
+        assert_close(to_np(h), href, TOL_GEMM, "fp8 h")
+        # the SwiGLU of the kernel's own bf16 h: one bf16 step of h near a
+        # row's largest activation already moves that row's a by ~1 %
+        assert_close(to_np(a), O.swiglu(to_np(h), None), TOL_GEMM, "fp8 a")
+    else:
+        aq, sa, wq, sw, d = _quantised_operands(rng, M, E, 256, 384)
+        dest = rng.permutation(M).astype(np.int32)
+        scale = rng.random(M).astype(np.float32)
+        out = ops.grouped_mm_fp8_unpermute(d["xq"], d["sx_t"], d["wq"], d["sw"], offs, f32_dev(scale),
+                                           torch.from_numpy(dest).to(DEV), M)
+        y = O.grouped_mm_fp8(aq, sa, wq, sw, np.cumsum(counts)) * scale[:, None]
+        ref = np.zeros_like(y)
+        ref[dest] = y
+        assert_close(to_np(out), ref, TOL_GEMM, "fp8 scatter")
+
+
 @pytest.mark.parametrize("K,score_before,limit", [(1, False, None), (2, False, None), (4, True, 0.05)])
 def test_moe_forward_fp8_vs_oracle(pkg, ops, K, score_before, limit):
     import importlib
