@@ -42,6 +42,11 @@
 //     stage s + 1's weight rows are issued into its buffer (its token rows
 //     and scales after the first token block's MFMAs): one stage ahead
 //     keeps the bounding DMA stream busy.
+//   * A wave computes only the 16-row token blocks of its half that hold
+//     tile rows (0, 2, 4, 6 or 8, rounded up to even): the k loop is
+//     instantiated per count and picked per tile.  The skipped blocks hold
+//     clamped copies of the tile's last row, whose products are never
+//     stored (short tiles of skewed expert loads).
 //   * Persistent workgroups, XCD-aware slots, flattened (tile, stage) DMA
 //     stream and the EPI_SCATTER metadata in LDS follow gemm_fwd.hip.
 #include <type_traits>
