@@ -588,28 +588,30 @@ int ttamd_grouped_mm_fp8_unpermute(const void* aq, const float* sa_t,
  * ------------------------------------------------------------------------ */
 
 /*
- * Arm the probe: the next grouped-GEMM main kernel of this process (any
+ * Arm the probe: the next grouped-GEMM main kernel this host thread
+ * launches (any
  * ttamd_grouped_mm* entry point, forward or dgrad, bf16 or fp8; not the
  * tile-table kernel before it) takes start_event and end_event as its own
  * start and end stamps (hipExtLaunchKernelGGL: nothing is enqueued between
  * kernels), then the probe disarms.  The events are caller-owned
  * hipEvent_t created with timing enabled (torch.cuda.Event(enable_timing=
  * True) after one record()).  NULL for both disarms.  While a launch chain
- * (ttamd_probe_launches) is armed it takes the launches first.  Not
- * thread-safe: one arming thread per process.
+ * (ttamd_probe_launches) is armed it takes the launches first.  The
+ * probe is per host thread: launches from other threads (for example
+ * torch's autograd worker running a backward) are not stamped.
  */
 int ttamd_probe_next_gemm(void* start_event, void* end_event);
 
 /*
- * Arm a chain over the next num_launches kernel launches of this process's
- * library calls (router, route, permute / quantise, grouped GEMMs, K-way
+ * Arm a chain over the next num_launches kernel launches of this host
+ * thread's library calls (router, route, permute / quantise, grouped GEMMs, K-way
  * sum: every kernel the entry points launch), whatever they are: launch i
  * takes events[2 i] and events[2 i + 1] as its start and end stamps
  * (caller-owned hipEvent_t with timing enabled; the stamps come from the
  * kernel's own dispatch), or runs unstamped when both are NULL, so a
  * caller can time one chosen kernel of a sequence.  A stamped dispatch
  * costs a few microseconds of GPU time.  0 <= num_launches <= 16; 0
- * disarms.  Not thread-safe.
+ * disarms.  Per host thread, as ttamd_probe_next_gemm.
  */
 int ttamd_probe_launches(void* const* events, int num_launches);
 

@@ -100,3 +100,34 @@ def test_launch_chain_null_pairs_and_gemm_probe():
     assert 0.5 * f_w2 < t_w2 < 2.0 * f_w2, (t_w2, f_w2)
     assert 0.5 * f_w13 < t_w13 < 2.0 * f_w13, (t_w13, f_w13)
     assert np.isfinite([t_w2, t_w13, f_w2, f_w13]).all()
+
+
+def test_probe_is_per_host_thread():
+    """A probe armed in one host thread is not taken by launches from
+    another (for example torch's autograd worker): the armed GEMM stamp lands
+    on the arming thread's next step, after the other thread's step."""
+    import threading
+
+    x, wr, w13, w2 = _inputs()
+    with torch.no_grad():
+        _step(x, wr, w13, w2)
+        torch.cuda.synchronize()
+        a, b = _events(2)
+        announce("GEMM probe armed in the main thread, a step from another thread")
+        ops.probe_next_gemm(a, b)
+
+        def other():
+            with torch.no_grad():
+                _step(x, wr, w13, w2)
+            torch.cuda.synchronize()
+
+        t = threading.Thread(target=other)
+        t.start()
+        t.join()
+        mid = torch.cuda.Event(enable_timing=True)
+        mid.record()
+        _step(x, wr, w13, w2)  # the main thread's next GEMM takes the probe
+        torch.cuda.synchronize()
+    ops.probe_next_gemm(None, None)
+    assert mid.elapsed_time(a) > 0, "the probe stamped the other thread's launch"
+    assert a.elapsed_time(b) > 0

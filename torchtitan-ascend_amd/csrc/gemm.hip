@@ -65,8 +65,10 @@ size_t gemm_workspace_bytes(int64_t M, int E) { return al256(gemm_plan_bytes(M, 
 
 static float* split_part_in(void* ws, int M, int E) { return (float*)((char*)ws + al256(gemm_plan_bytes(M, E))); }
 
+// One probe per host thread: a thread's arming stamps only the launches
+// that thread makes (other threads' launches never see it).
 Probe& probe() {
-  static Probe p;
+  thread_local Probe p;
   return p;
 }
 

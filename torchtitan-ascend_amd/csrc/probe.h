@@ -5,7 +5,8 @@
 // A probed launch passes its event pair to hipExtLaunchKernelGGL, which
 // stamps the kernel's own start and end from its dispatch: nothing is
 // enqueued between kernels, so the timed kernels run back to back exactly
-// as unprobed ones do.  Two ways to arm it, from one host thread:
+// as unprobed ones do.  The probe is per host thread (the launches of the
+// thread that armed it).  Two ways to arm it:
 //   * the next grouped-GEMM main kernel (forward, dgrad, fp8) takes the
 //     pair (gemm_start, gemm_end), then the probe disarms;
 //   * a chain over the next n kernel launches of the library, whatever they
