@@ -388,13 +388,10 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
 
 template <int EPI>
 hipError_t launch_fp8(const Fp8Args& a, hipStream_t stream) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t err = hipFuncSetAttribute((const void*)gg_fp8_kernel<EPI>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, LDS_TOTAL);
-    if (err != hipSuccess) return err;
-    attr_set = true;
-  }
+  // set once per process (thread-safe static initialisation)
+  static const hipError_t attr_err =
+      hipFuncSetAttribute((const void*)gg_fp8_kernel<EPI>, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_TOTAL);
+  if (attr_err != hipSuccess) return attr_err;
   const int grid = (num_cus() + 7) & ~7;
   return launch_k(true, gg_fp8_kernel<EPI>, dim3(grid), dim3(FTHREADS), LDS_TOTAL, stream, a);
 }

@@ -776,20 +776,15 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
 
 template <int EPI, bool PT = false, bool GATHER = false>
 hipError_t launch_fwd(FwdArgs a, hipStream_t stream) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t err = hipFuncSetAttribute((const void*)gg_fwd_kernel<EPI, PT, GATHER>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, LDS_TOTAL);
-    if (err != hipSuccess) return err;
-    attr_set = true;
-  }
+  // set once per process (thread-safe static initialisation)
+  static const hipError_t attr_err =
+      hipFuncSetAttribute((const void*)gg_fwd_kernel<EPI, PT, GATHER>, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_TOTAL);
+  if (attr_err != hipSuccess) return attr_err;
   const int grid = (num_cus() + 7) & ~7;
   return launch_k(true, gg_fwd_kernel<EPI, PT, GATHER>, dim3(grid), dim3(FTHREADS), LDS_TOTAL, stream, a);
 }
 
 }  // namespace
-
-static int g_num_cus = 0;
 
 // Pieces per split leftover tile at most (TTAMD_GEMM_SPLIT=1 turns the
 // split off, for A/B timing).
@@ -802,15 +797,17 @@ static int split_max() {
   return v;
 }
 
+// CUs of the device current at the first call (thread-safe static
+// initialisation; every device of a process is the same part).
 int num_cus() {
-  if (g_num_cus == 0) {
+  static const int cus = [] {
     int dev = 0, n = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
-    g_num_cus = n;
-  }
-  return g_num_cus;
+    return n;
+  }();
+  return cus;
 }
 
 hipError_t launch_fwd_gemm(int epi, const FwdGemm& g, hipStream_t stream) {

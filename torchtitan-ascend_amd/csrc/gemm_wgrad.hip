@@ -329,13 +329,10 @@ __global__ __launch_bounds__(THREADS, 1) void gg_wgrad_dma_kernel(const WgradDma
 }  // namespace
 
 hipError_t launch_wgrad_dma(const WgradDmaArgs& a, hipStream_t stream) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t err = hipFuncSetAttribute((const void*)gg_wgrad_dma_kernel,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, LDS_TOTAL);
-    if (err != hipSuccess) return err;
-    attr_set = true;
-  }
+  // set once per process (thread-safe static initialisation)
+  static const hipError_t attr_err =
+      hipFuncSetAttribute((const void*)gg_wgrad_dma_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, LDS_TOTAL);
+  if (attr_err != hipSuccess) return attr_err;
   const int grid = (num_cus() + 7) & ~7;
   return launch_k(false, gg_wgrad_dma_kernel, dim3(grid), dim3(THREADS), LDS_TOTAL, stream, a);
 }

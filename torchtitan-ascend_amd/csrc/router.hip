@@ -512,13 +512,10 @@ template <int EB>
 hipError_t launch_gemm_eb(const RouterGemmArgs& a, int S, hipStream_t stream) {
   constexpr int lds = router_nst<EB>() * (RT + 32 * EB) * 128;
   static_assert(lds <= 160 * 1024, "router LDS");
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t err = hipFuncSetAttribute((const void*)router_gemm_kernel<EB>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (err != hipSuccess) return err;
-    attr_set = true;
-  }
+  // set once per process (thread-safe static initialisation)
+  static const hipError_t attr_err =
+      hipFuncSetAttribute((const void*)router_gemm_kernel<EB>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (attr_err != hipSuccess) return attr_err;
   return launch_k(false, router_gemm_kernel<EB>, dim3((a.T + RT - 1) / RT, S), dim3(RTHREADS), lds, stream, a);
 }
 
