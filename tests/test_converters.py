@@ -163,3 +163,32 @@ def test_dispatcher_converter_passes_the_degree():
     mc = _model()
     pkg.HipTokenDispatcherConverter(pkg.HipTokenDispatcherConverter.Config(expert_parallel_degree=1)).convert(mc)
     assert mc.layers[0].token_dispatcher.expert_parallel_degree == 1
+
+
+def test_expert_tp_degree_from_dtensor_placements(tmp_path, monkeypatch):
+    """w2 sharded on its hidden dim (Shard(2), npu_gmm.py:79-83) over a mesh
+    of one rank holds the whole weight and runs as is; a degree above one
+    needs the reference's all-reduce and raises instead of returning a
+    partial sum."""
+    import torch.distributed as dist
+    from torch.distributed.device_mesh import init_device_mesh
+    from torch.distributed.tensor import Replicate, Shard, distribute_tensor
+
+    GE = importlib.import_module("torchtitan-ascend_amd.grouped_experts")
+    dist.init_process_group("gloo", init_method=f"file://{tmp_path}/pg", rank=0, world_size=1)
+    try:
+        mesh = init_device_mesh("cpu", (1,))
+        w = torch.randn(4, 16, 8)
+        local, tp = GE._local(distribute_tensor(w, mesh, [Shard(2)]))
+        assert tp == 1 and torch.equal(local, w)
+        assert GE._local(distribute_tensor(w, mesh, [Replicate()]))[1] == 1
+        assert GE._local(w)[1] == 1
+    finally:
+        dist.destroy_process_group()
+    m = pkg.HipGroupedExperts.Config(
+        dim=256, hidden_dim=128, num_experts=4,
+        token_dispatcher=pkg.HipTokenDispatcher.Config(num_experts=4, top_k=1),
+    ).build()
+    monkeypatch.setattr(GE, "_local", lambda p: (p, 2))
+    with pytest.raises(NotImplementedError, match="degree 2"):
+        m._weights()

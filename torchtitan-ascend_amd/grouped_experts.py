@@ -25,17 +25,22 @@ from .state_dict import upstream_to_fused
 from .token_dispatcher import HipTokenDispatcher
 
 
-def _local(p: torch.Tensor) -> tuple[torch.Tensor, bool]:
-    """DTensor -> local shard; reports whether the shard splits the hidden dim (expert TP)."""
+def _local(p: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """DTensor -> (local shard, expert-TP degree): the number of shards the
+    hidden dim (dim 2 of w2) is split into, 1 when it is not split
+    (npu_gmm.py:74-83 detects the same Shard(2) placement)."""
     try:
         from torch.distributed.tensor import DTensor
         from torch.distributed.tensor.placement_types import Shard
     except ImportError:  # pragma: no cover
-        return p, False
+        return p, 1
     if isinstance(p, DTensor):
-        is_tp = any(isinstance(pl, Shard) and pl.dim == 2 for pl in p.placements)
-        return p.to_local(), is_tp
-    return p, False
+        tp = 1
+        for mesh_dim, pl in enumerate(p.placements):
+            if isinstance(pl, Shard) and pl.dim == 2:
+                tp *= p.device_mesh.size(mesh_dim)
+        return p.to_local(), tp
+    return p, 1
 
 
 def _load_upstream_w1_w3(state_dict, prefix, *args, **kwargs):
@@ -71,8 +76,13 @@ class HipGroupedExperts(Module):
     def _weights(self):
         w2, tp2 = _local(self.w2)
         w13, _ = _local(self.w13)
-        if tp2:
-            raise NotImplementedError("expert tensor parallelism (w2 sharded on dim 2) needs a collective")
+        if tp2 > 1:
+            # npu_gmm.py:93-96 all-reduces the partial outputs over the TP
+            # group; a mesh of one rank holds the whole hidden dim and runs
+            # as is
+            raise NotImplementedError(
+                f"expert tensor parallelism of degree {tp2} (w2 sharded on dim 2) needs an all-reduce "
+                "across the TP group; this build runs the experts of one GPU")
         return w13, w2
 
     def _experts_forward(self, x, num_tokens_per_expert):
