@@ -502,7 +502,12 @@ int ttamd_grouped_mm_dgrad_swiglu(const void* dy, const void* w2,
  * Grouped wgrad: dw[e, n, k] = sum_{m in group e} dy[m, n] * x[m, k].
  * dy [M, N], x [M, K] bf16; dw [E, N, K] fp32 (dw_is_fp32=1) or bf16.
  * Experts with no rows get zeros.  N % 128 == 0, K % 128 == 0.
- * Deterministic (no atomics).
+ * workspace: NULL, or ttamd_gemm_workspace_bytes(num_rows, num_experts)
+ * bytes (contents need no initialisation): with it, the output tiles left
+ * over after the last full round of the persistent walk are cut along the
+ * rows into pieces that run on the otherwise idle CUs.  Deterministic
+ * either way: the pieces' fp32 sums are added in piece order, whichever
+ * finishes last (one arrival counter per leftover tile).
  */
 int ttamd_grouped_mm_wgrad(const void* dy, const void* x, const int32_t* offs,
                            int64_t num_rows, int num_experts, int64_t n,

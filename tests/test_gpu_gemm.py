@@ -3,6 +3,8 @@ accumulation).  Tolerance: max relative error (max|got-ref| / max|ref|)
 <= 2e-2 for bf16, the bound the path is specified to."""
 from __future__ import annotations
 
+import importlib
+
 import numpy as np
 import pytest
 import torch
@@ -387,3 +389,55 @@ def test_probe_times_one_gemm_kernel(ops):
     with pytest.raises(ValueError):
         ops.probe_next_gemm(p0, None)
 
+
+
+# Output-tile counts that leave a partial last round of the persistent walk
+# on 256 CUs, with enough rows for the tail split to cut the leftover tiles
+# along the rows: one expert over 2048 rows (300 tiles: 44 left over, 4
+# pieces of 8 stages), and three experts whose leftover tiles belong to a
+# loaded expert (2 pieces of 11 stages) or to an expert without rows.
+WGRAD_SPLIT_CASES = [
+    ([2048], 3840, 5120),
+    ([1900, 0, 1400], 2560, 2560),
+    ([1900, 1400, 0], 2560, 2560),
+]
+
+
+@pytest.mark.parametrize("counts,N,K", WGRAD_SPLIT_CASES)
+def test_grouped_mm_wgrad_tail_split(ops, counts, N, K):
+    """The leftover output tiles of a walk that ends in a partial round are
+    cut along the expert's rows into pieces summed in piece order: against
+    the oracle per expert slice, bit-identical on a second call (whichever
+    piece arrives last), exact zeros for an expert without rows, and (fp32)
+    not bit-identical to the unsplit kernel, so the pieces did run."""
+    import ctypes
+
+    from gpu_util import assert_close
+
+    lib = importlib.import_module("torchtitan-ascend_amd._lib")
+    counts = np.array(counts)
+    M, E = int(counts.sum()), counts.size
+    rng = np.random.default_rng(M + N + K)
+    dy = rand_bf16(rng, (M, N))
+    x = rand_bf16(rng, (M, K))
+    ref = O.grouped_wgrad(dy, x, np.cumsum(counts), E)
+    dyd, xd, offs = bf16_dev(dy), bf16_dev(x), _offs(counts)
+    for out_dtype in (torch.float32, torch.bfloat16):
+        announce(f"wgrad tail split counts={counts.tolist()} N={N} K={K} {out_dtype}")
+        a = ops.grouped_mm_wgrad(dyd, xd, offs, E, out_dtype)
+        b = ops.grouped_mm_wgrad(dyd, xd, offs, E, out_dtype)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), "split sums differ between calls"
+        got = to_np(a)
+        for e in np.where(counts == 0)[0]:
+            assert not np.any(got[e]), f"expert {e} has no rows but a nonzero gradient"
+        assert_close(got, ref, TOL, f"wgrad split {out_dtype}")
+        if out_dtype == torch.float32:
+            plain = torch.empty_like(a)
+            lib.call("ttamd_grouped_mm_wgrad", ctypes.c_void_p(dyd.data_ptr()), ctypes.c_void_p(xd.data_ptr()),
+                     ctypes.c_void_p(offs.data_ptr()), M, E, N, K, ctypes.c_void_p(plain.data_ptr()), 1, None, 0,
+                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            torch.cuda.synchronize()
+            assert_close(to_np(plain), ref, TOL, "wgrad unsplit")
+            if counts[-1] > 0:
+                assert not torch.equal(a, plain), "the tail split did not run"

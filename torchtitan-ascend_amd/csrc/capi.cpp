@@ -699,9 +699,9 @@ int ttamd_grouped_mm_wgrad(const void* dy, const void* x, const int32_t* offs, i
                            int num_experts, int64_t n, int64_t k, void* dw, int dw_is_fp32,
                            void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "ttamd_grouped_mm_wgrad";
-  (void)workspace;
-  (void)workspace_bytes;
   TRY(check_gemm_common(fn, offs, num_rows, num_experts));
+  if (workspace != nullptr)
+    TRY(check_ws(fn, workspace, workspace_bytes, ttamd::gemm_workspace_bytes(num_rows, num_experts)));
   TRY(check_dim(fn, "n", n, 128));
   TRY(check_dim(fn, "k", k, 128));
   TRY(check_rows(fn, "dy", dy, num_rows, n));
@@ -712,7 +712,7 @@ int ttamd_grouped_mm_wgrad(const void* dy, const void* x, const int32_t* offs, i
   REQUIRE(num_rows * n * 2 <= (int64_t)0xffffffffLL && num_rows * k * 2 <= (int64_t)0xffffffffLL,
           "%s: dy and x must each stay below 4 GiB", fn);
   return check_hip(ttamd::launch_grouped_mm_wgrad(dy, x, offs, (int)num_rows, num_experts, (int)n,
-                                                  (int)k, dw, dw_is_fp32 != 0,
+                                                  (int)k, dw, dw_is_fp32 != 0, workspace,
                                                   (hipStream_t)stream),
                    fn);
 }

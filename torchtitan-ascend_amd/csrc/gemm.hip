@@ -9,6 +9,8 @@
 //   :17-18, :31, :38  torch._grouped_mm(x, w.transpose(-2, -1), offs)
 //   :32-36            optional clamp with swiglu_limit
 //   :37               npu_swiglu: silu(gate) * up, gate = first H columns
+#include <algorithm>
+
 #include "common.h"
 #include "gemm_common.h"
 #include "kernels.h"
@@ -321,13 +323,36 @@ hipError_t launch_grouped_mm_dgrad_swiglu(const void* dy, const void* w2, const 
 }
 
 hipError_t launch_grouped_mm_wgrad(const void* dy, const void* x, const int* offs, int M, int E,
-                                   int N, int K, void* dw, bool fp32, hipStream_t stream) {
+                                   int N, int K, void* dw, bool fp32, void* ws, hipStream_t stream) {
   WgradDmaArgs a = {};
   a.dy = (const bf16_t*)dy; a.lddy = N;
   a.x = (const bf16_t*)x; a.ldx = K;
   a.offs = offs; a.E = E; a.M = M; a.N = N; a.K = K;
   a.n_tiles = (N + 255) / 256; a.k_tiles = (K + 255) / 256;
   a.dw = dw; a.dw_fp32 = fp32 ? 1 : 0;
+  a.split_np = 1;
+  if (ws != nullptr) {
+    // Tail split for a walk of at most kSplitMaxRounds full rounds with
+    // tiles left over: up to kSplitMaxPieces pieces per leftover tile, so
+    // that the pieces fill the otherwise idle workgroups, each piece of at
+    // least kSplitMinStages stages of the average expert's rows.
+    const int G = (num_cus() + 7) & ~7;
+    const int ntiles = E * a.n_tiles * a.k_tiles;
+    const int R = ntiles / G, rt = ntiles - R * G;
+    if (rt > 0 && rt <= kSplitTiles && R <= kSplitMaxRounds) {
+      int np = std::min(kSplitMaxPieces, G / rt);
+      const int avg_stages = (M / E + 63) / 64;
+      while (np > 1 && avg_stages < np * kSplitMinStages) --np;
+      if (np > 1) {
+        TileTable tt = tile_table_in(ws);
+        hipError_t err = launch_split_cnt_zero(tt.split_cnt, rt, stream);
+        if (err != hipSuccess) return err;
+        a.part = split_part_in(ws, M, E);
+        a.split_cnt = tt.split_cnt;
+        a.split_np = np;
+      }
+    }
+  }
   return launch_wgrad_dma(a, stream);
 }
 

@@ -211,8 +211,17 @@ struct WgradDmaArgs {
   int n_tiles, k_tiles;  // per expert, 256-wide
   void* dw;              // [E][N][K]
   int dw_fp32;
+  // Tail split (split_np > 1): the tiles left over after the last full
+  // round are cut along the reduction rows into split_np pieces; each
+  // piece writes its fp32 sums (kSplitPartBytes at most) to `part` and
+  // counts its arrival in split_cnt[leftover tile] (zero on entry, left at
+  // zero).  split_np <= 1: no split.
+  float* part;
+  int* split_cnt;
+  int split_np;
 };
 hipError_t launch_wgrad_dma(const WgradDmaArgs& a, hipStream_t stream);
+hipError_t launch_split_cnt_zero(int* split_cnt, int n, hipStream_t stream);
 
 // Kernel arguments of the fp8 forward GEMM (gemm_fp8.hip).  Activations and
 // weights are e4m3 bytes; strides are in bytes for them, in elements for

@@ -27,6 +27,12 @@
 //     expert.
 //     An expert without rows still takes one (fully masked) stage, so its
 //     gradient tile is written as zeros.
+//   * Tail split (as in gemm_fwd.hip): with a workspace, the tiles left over
+//     after the last full round are cut along the expert's rows into pieces
+//     of consecutive stages, run on the otherwise idle workgroups; each
+//     piece writes its fp32 sums to the workspace and counts its arrival,
+//     and the last to arrive adds all of them in piece order (the same sum
+//     whichever arrives last) and runs the epilogue.
 #include "common.h"
 #include "dma_asm.h"
 #include "gemm_common.h"
@@ -57,6 +63,8 @@ constexpr int kStripN = 4;  // n tiles per strip of the tile order
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+typedef __attribute__((address_space(1))) int gint_t;
+typedef __attribute__((address_space(1))) floatx4_t gfloatx4_t;
 
 __device__ __forceinline__ int ptswz(int m) { return 4 * ((m ^ (m >> 3)) & 3); }
 
@@ -76,8 +84,17 @@ __global__ __launch_bounds__(THREADS, 1) void gg_wgrad_dma_kernel(const WgradDma
   const int slot = (b & 7) * (G >> 3) + (b >> 3);
   const int per_e = a.n_tiles * a.k_tiles;
   const int ntiles = a.E * per_e;
-  const int nmy = slot < ntiles ? (ntiles - slot + G - 1) / G : 0;
+  // Tail split: R full rounds, rt tiles left over; piece j of leftover tile
+  // t runs on slot j * rt + t after the slot's R whole tiles.
+  const int R = ntiles / G;
+  const int rt = ntiles - R * G;
+  const int np = (a.split_np > 1 && rt > 0 && rt <= kSplitTiles && a.split_np * rt <= G) ? a.split_np : 1;
+  const bool has_piece = np > 1 && slot < rt * np;
+  const int nfull = np > 1 ? R : (slot < ntiles ? (ntiles - slot + G - 1) / G : 0);
+  const int nmy = nfull + (has_piece ? 1 : 0);
   if (nmy == 0) return;
+  const int pc_t = has_piece ? slot % rt : 0;  // leftover tile of the piece
+  const int pc_j = has_piece ? slot / rt : 0;  // piece index
   const uint32_t lds0 = lds_addr(smem);
 
   // tile round r -> (expert, n tile, k tile, first row, end row, stages)
@@ -86,7 +103,7 @@ __global__ __launch_bounds__(THREADS, 1) void gg_wgrad_dma_kernel(const WgradDma
   };
   auto tile_of = [&](int r) {
     Tile t;
-    const int id = r * G + slot;
+    const int id = r < nfull ? r * G + slot : R * G + pc_t;
     t.e = id / per_e;
     const int rem = id - t.e * per_e;
     // Within an expert, strips of kStripN n tiles, k tile major inside a
@@ -104,6 +121,15 @@ __global__ __launch_bounds__(THREADS, 1) void gg_wgrad_dma_kernel(const WgradDma
     t.m0 = min(max(t.m0, 0), a.M);
     t.m1 = min(max(t.m1, t.m0), a.M);
     t.nks = max(1, (t.m1 - t.m0 + TK - 1) / TK);
+    if (r >= nfull) {
+      // piece pc_j: stages [k0, k1) of the tile's rows (an empty share runs
+      // one fully masked stage and contributes zeros)
+      const int k0 = pc_j * t.nks / np, k1 = (pc_j + 1) * t.nks / np;
+      const int m_end = t.m1;
+      t.m1 = min(t.m0 + TK * k1, m_end);
+      t.m0 = min(t.m0 + TK * k0, m_end);
+      t.nks = max(1, k1 - k0);
+    }
     return t;
   };
 
@@ -246,6 +272,79 @@ __global__ __launch_bounds__(THREADS, 1) void gg_wgrad_dma_kernel(const WgradDma
       mfma(f1);
     }
 
+    // ---- split leftover tile: publish this piece's sums; the last piece to
+    //      arrive adds all of them in piece order and runs the epilogue.
+    //      The partials are written back from this XCD's L2 (release) before
+    //      the arrival is counted, and the last piece invalidates its caches
+    //      (acquire) before it reads the others'; it resets the counter.
+    if (np > 1 && r >= nfull) {
+      constexpr int NV4 = NPB * NJ * 4;                   // float4 per lane
+      constexpr uint32_t WAVE_BYTES = NV4 * 64 * 16;      // 32 KB
+      constexpr uint64_t PIECE_BYTES = (uint64_t)WAVES * WAVE_BYTES;  // 256 KB
+      static_assert(PIECE_BYTES <= kSplitPartBytes, "partial of a piece");
+      // The bases are made opaque here so that no address is computed (and
+      // kept live) in the k loop.
+      uint64_t pw = (uint64_t)a.part + (uint64_t)w * WAVE_BYTES;
+      asm volatile("" : "+s"(pw));
+      uint32_t loff = (uint32_t)l * 16u;
+      asm volatile("" : "+v"(loff));
+      auto piece = [&](int j) { return pw + (uint64_t)(pc_t * np + j) * PIECE_BYTES; };
+      const uint64_t mine = piece(pc_j);
+#pragma unroll
+      for (int pb = 0; pb < NPB; ++pb)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            *(gfloatx4_t*)(mine + (uint32_t)(((pb * NJ + j) * 4 + g) * 1024) + loff) =
+                floatx4_t{acc[pb][j][4 * g], acc[pb][j][4 * g + 1], acc[pb][j][4 * g + 2], acc[pb][j][4 * g + 3]};
+      wait_vm<0>();  // this wave's partial has reached L2; every DMA has landed
+      __syncthreads();
+      // (the stage buffers are idle: no DMA is issued after the last unit)
+      int* flag = (int*)smem;
+      if (w == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        gint_t* cnt = (gint_t*)(a.split_cnt + pc_t);
+        int old = 0;
+        if (l == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __builtin_amdgcn_readfirstlane(old);
+        if (old == np - 1) {
+          if (l == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+          // the cache invalidation has completed before the barrier below
+          // lets the other waves load the partials
+          wait_vm<0>();
+        }
+        if (l == 0) *flag = (old == np - 1);
+      }
+      __syncthreads();
+      if (__builtin_amdgcn_readfirstlane(*flag) == 0) return;
+#pragma unroll
+      for (int pb = 0; pb < NPB; ++pb)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[pb][j][v] = 0.f;
+      // the sum in piece order, one 16-float block (four loads) at a time
+      for (int jp = 0; jp < np; ++jp) {
+        const uint64_t src = piece(jp);
+#pragma unroll
+        for (int pb = 0; pb < NPB; ++pb)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            floatx4_t v[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+              v[g] = *(const gfloatx4_t*)(src + (uint32_t)(((pb * NJ + j) * 4 + g) * 1024) + loff);
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) acc[pb][j][4 * g + i] += v[g][i];
+            __builtin_amdgcn_sched_barrier(0);
+          }
+      }
+    }
+
     // ---- epilogue: acc[pb][j][4g + i] = dw[e][n][k], n = nt*TQ + brow[j] +
     //      lane % 32, k = kt*TP + arow[pb] + 8g + 4 (lane / 32) + i.
     int er32 = l & 31;
@@ -326,7 +425,17 @@ __global__ __launch_bounds__(THREADS, 1) void gg_wgrad_dma_kernel(const WgradDma
   wait_vm<0>();
 }
 
+// Arrival counters of the split tail tiles to zero (a kernel, not a memset,
+// so that the sequence can be captured in a HIP graph).
+__global__ __launch_bounds__(256) void split_cnt_zero_kernel(int* __restrict__ cnt, int n) {
+  for (int i = threadIdx.x; i < n; i += 256) cnt[i] = 0;
+}
+
 }  // namespace
+
+hipError_t launch_split_cnt_zero(int* split_cnt, int n, hipStream_t stream) {
+  return launch_k(false, split_cnt_zero_kernel, dim3(1), dim3(256), 0, stream, split_cnt, n);
+}
 
 hipError_t launch_wgrad_dma(const WgradDmaArgs& a, hipStream_t stream) {
   // set once per process (thread-safe static initialisation)

@@ -122,8 +122,10 @@ hipError_t launch_grouped_mm_dgrad_swiglu(const void* dy, const void* w2, const 
                                           const int* offs, int M, int E, int D, int H,
                                           float limit, void* dh, void* a_out, void* ws,
                                           hipStream_t stream);
+// ws: NULL (no tail split) or gemm_workspace_bytes(M, E) bytes (the
+// leftover tiles' partial sums and arrival counters).
 hipError_t launch_grouped_mm_wgrad(const void* dy, const void* x, const int* offs, int M, int E,
-                                   int N, int K, void* dw, bool fp32, hipStream_t stream);
+                                   int N, int K, void* dw, bool fp32, void* ws, hipStream_t stream);
 
 // fp8 e4m3 path (quant.hip, gemm_fp8.hip via gemm.hip)
 hipError_t launch_quantize_rows(const void* in, const int* src_index, int src_div, const float* row_mul,

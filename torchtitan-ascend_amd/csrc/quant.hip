@@ -186,9 +186,8 @@ hipError_t launch_quantize_blocks(const void* w, int E, int N, int K, void* q_ou
                                   hipStream_t stream) {
   const int64_t nblk = (int64_t)E * (N / 128) * (K / 128);
   if (nblk == 0) return hipSuccess;
-  hipLaunchKernelGGL(quantize_blocks_kernel, dim3((unsigned)nblk), dim3(256), 0, stream, (const uint4*)w, N,
-                     K, (uint2*)q_out, scale);
-  return hipGetLastError();
+  return launch_k(false, quantize_blocks_kernel, dim3((unsigned)nblk), dim3(256), 0, stream, (const uint4*)w, N,
+                  K, (uint2*)q_out, scale);
 }
 
 }  // namespace ttamd

@@ -665,17 +665,17 @@ hipError_t launch_router_backward(const float* grad, const int64_t* idx, const v
   b.dlogits = dlog;
   b.ldd = P;
   const dim3 grid((T + 15) / 16);
-  if (E <= 32) hipLaunchKernelGGL(router_backward_kernel<2>, grid, dim3(256), 0, stream, b);
-  else if (E <= 64) hipLaunchKernelGGL(router_backward_kernel<4>, grid, dim3(256), 0, stream, b);
-  else if (E <= 128) hipLaunchKernelGGL(router_backward_kernel<8>, grid, dim3(256), 0, stream, b);
-  else hipLaunchKernelGGL(router_backward_kernel<16>, grid, dim3(256), 0, stream, b);
-  hipError_t err = hipGetLastError();
+  hipError_t err;
+  if (E <= 32) err = launch_k(false, router_backward_kernel<2>, grid, dim3(256), 0, stream, b);
+  else if (E <= 64) err = launch_k(false, router_backward_kernel<4>, grid, dim3(256), 0, stream, b);
+  else if (E <= 128) err = launch_k(false, router_backward_kernel<8>, grid, dim3(256), 0, stream, b);
+  else err = launch_k(false, router_backward_kernel<16>, grid, dim3(256), 0, stream, b);
   if (err != hipSuccess) return err;
   const int cpr = D / 8;
   const int pg = min(2048, (P * cpr + 255) / 256);
-  hipLaunchKernelGGL(router_pad_kernel, dim3(pg), dim3(256), 0, stream, (const uint4*)w, E, P, cpr, (uint4*)w_pad,
-                     offs1, T, offsg, G);
-  if ((err = hipGetLastError()) != hipSuccess) return err;
+  if ((err = launch_k(false, router_pad_kernel, dim3(pg), dim3(256), 0, stream, (const uint4*)w, E, P, cpr,
+                      (uint4*)w_pad, offs1, T, offsg, G)) != hipSuccess)
+    return err;
   if (dx) {
     // dx[t][d] = sum_e dlogits[t][e] w[e][d]: dgrad with the weight [1][P][D]
     // (a reduction of P <= 1024 is at most 16 k stages: not worth splitting)
@@ -701,9 +701,8 @@ hipError_t launch_router_backward(const float* grad, const int64_t* idx, const v
     wa.dw_fp32 = 1;
     if ((err = launch_wgrad_dma(wa, stream)) != hipSuccess) return err;
     const int n4 = E * (D / 4);
-    hipLaunchKernelGGL(router_dw_reduce_kernel, dim3(min(2048, (n4 + 255) / 256)), dim3(256), 0, stream,
-                       (const float4*)dw_part, G, NR, E, D / 4, dw, dw_fp32 ? 1 : 0);
-    err = hipGetLastError();
+    err = launch_k(false, router_dw_reduce_kernel, dim3(min(2048, (n4 + 255) / 256)), dim3(256), 0, stream,
+                   (const float4*)dw_part, G, NR, E, D / 4, dw, dw_fp32 ? 1 : 0);
   }
   return err;
 }

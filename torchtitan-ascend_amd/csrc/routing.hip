@@ -636,8 +636,7 @@ hipError_t launch_invert_perm(const int* sorted, int M, int* inv, hipStream_t st
   if (M == 0) return hipSuccess;
   int g = (M + kMoveThreads - 1) / kMoveThreads;
   if (g > 4096) g = 4096;
-  hipLaunchKernelGGL(invert_perm_kernel, dim3(g), dim3(kMoveThreads), 0, stream, sorted, M, inv);
-  return hipGetLastError();
+  return launch_k(false, invert_perm_kernel, dim3(g), dim3(kMoveThreads), 0, stream, sorted, M, inv);
 }
 
 // out[t] = sum_k w(t,k) * in[j(t,k)],  j = inverse ? inverse[t*topk+k] : t*topk+k.
@@ -732,10 +731,8 @@ hipError_t launch_rowdot(const void* a, const void* b, const int* bidx, int bdiv
   if (rows == 0) return hipSuccess;
   int64_t g = ((int64_t)rows * kWave + kMoveThreads - 1) / kMoveThreads;
   if (g > 8192) g = 8192;
-  hipLaunchKernelGGL(rowdot_kernel, dim3((int)g), dim3(kMoveThreads), 0, stream,
-                     (const uint4*)a, (const uint4*)b, bidx, bdiv, out_by_bidx ? 1 : 0, rows,
-                     n_b, n_out, hidden / 8, out);
-  return hipGetLastError();
+  return launch_k(false, rowdot_kernel, dim3((int)g), dim3(kMoveThreads), 0, stream, (const uint4*)a,
+                  (const uint4*)b, bidx, bdiv, out_by_bidx ? 1 : 0, rows, n_b, n_out, hidden / 8, out);
 }
 
 // ---------------------------------------------------------------------------
@@ -786,9 +783,8 @@ hipError_t launch_group_labels(const int* counts_group, int G, int E_loc, int ro
   if (rows == 0) return hipSuccess;
   int g = (rows + kMoveThreads - 1) / kMoveThreads;
   if (g > 1024) g = 1024;
-  hipLaunchKernelGGL(group_labels_kernel, dim3(g), dim3(kMoveThreads), 0, stream, counts_group, G,
-                     E_loc, rows, labels);
-  return hipGetLastError();
+  return launch_k(false, group_labels_kernel, dim3(g), dim3(kMoveThreads), 0, stream, counts_group, G, E_loc,
+                  rows, labels);
 }
 
 // ---------------------------------------------------------------------------
@@ -902,23 +898,15 @@ hipError_t launch_router_topk(const float* logits, const float* bias, int T, int
   int64_t g = ((int64_t)T * kWave + kMoveThreads - 1) / kMoveThreads;
   if (g > 8192) g = 8192;
   const int per = (E + kWave - 1) / kWave;
-#define TTAMD_TOPK_CASE(P)                                                                     \
-  hipLaunchKernelGGL(router_topk_kernel<P>, dim3((int)g), dim3(kMoveThreads), 0, stream, logits, \
-                     bias, T, E, K, score_func, renorm, renorm_eps, route_scale, top_scores,    \
-                     top_idx)
-  if (per <= 1) {
-    TTAMD_TOPK_CASE(1);
-  } else if (per <= 2) {
-    TTAMD_TOPK_CASE(2);
-  } else if (per <= 4) {
-    TTAMD_TOPK_CASE(4);
-  } else if (per <= 8) {
-    TTAMD_TOPK_CASE(8);
-  } else {
-    TTAMD_TOPK_CASE(kTopkMaxPerLane);
-  }
-#undef TTAMD_TOPK_CASE
-  return hipGetLastError();
+  auto go = [&](auto kernel) {
+    return launch_k(false, kernel, dim3((int)g), dim3(kMoveThreads), 0, stream, logits, bias, T, E, K, score_func,
+                    renorm, renorm_eps, route_scale, top_scores, top_idx);
+  };
+  if (per <= 1) return go(router_topk_kernel<1>);
+  if (per <= 2) return go(router_topk_kernel<2>);
+  if (per <= 4) return go(router_topk_kernel<4>);
+  if (per <= 8) return go(router_topk_kernel<8>);
+  return go(router_topk_kernel<kTopkMaxPerLane>);
 }
 
 }  // namespace ttamd

@@ -799,9 +799,10 @@ def grouped_mm_wgrad(
     if out_dtype not in (torch.float32, _BF16):
         raise TypeError("wgrad output must be float32 or bfloat16")
     dw = torch.empty(num_experts, N, K, dtype=out_dtype, device=dev)
+    ws = _gemm_ws(M, num_experts, dev)  # tail split of the leftover output tiles
     _lib.call(
         "ttamd_grouped_mm_wgrad", _p(dy), _p(x), _p(offs), M, num_experts, N, K, _p(dw),
-        int(out_dtype == torch.float32), None, 0, _stream(dev),
+        int(out_dtype == torch.float32), _p(ws), ws.numel(), _stream(dev),
     )
     return dw
 
