@@ -333,35 +333,43 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
       const int gq = row0 + 128 * wq + 16 * jb + er16;
       const bool row_ok = gq < row1;
       if constexpr (EPI == EPI_SWIGLU) {
-        const bool clamp = (a.limit == a.limit);
         const float L = a.limit;
         // wave-uniform: this quarter's 32 gate columns lie past H (H % 128 == 64)
         if (pt * 128 + 32 * wp >= a.hidden) continue;
+        // The clamp (swiglu_limit) is wave-uniform too: one code path each,
+        // so that the unclamped SwiGLU carries no min / max per value.
+        auto swiglu_rows = [&](auto clampc) {
+          constexpr bool CLAMP = decltype(clampc)::value;
 #pragma unroll
-        for (int pb = 0; pb < 2; ++pb) {
-          const int col = pt * 128 + arow[pb] + 4 * eg4;
-          float av[4], gv[4], uv[4];
+          for (int pb = 0; pb < 2; ++pb) {
+            const int col = pt * 128 + arow[pb] + 4 * eg4;
+            float av[4], gv[4], uv[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            gv[i] = round_bf16(acc[pb][jb][i]);
-            uv[i] = round_bf16(acc[pb + 2][jb][i]);
-            float gc = gv[i], uc = uv[i];
-            if (clamp) {
-              gc = fminf(gc, L);
-              uc = fminf(fmaxf(uc, -L), L);
+            for (int i = 0; i < 4; ++i) {
+              gv[i] = round_bf16(acc[pb][jb][i]);
+              uv[i] = round_bf16(acc[pb + 2][jb][i]);
+              float gc = gv[i], uc = uv[i];
+              if constexpr (CLAMP) {
+                gc = fminf(gc, L);
+                uc = fminf(fmaxf(uc, -L), L);
+              }
+              av[i] = silu_f(gc) * uc;
             }
-            av[i] = silu_f(gc) * uc;
-          }
-          if (row_ok) {
-            bf16_t* orow = a.out + (int64_t)gq * a.ldo + col;
-            *(uint2*)orow = make_uint2(pack_bf16x2(av[0], av[1]), pack_bf16x2(av[2], av[3]));
-            if (a.h_out) {
-              bf16_t* hrow = a.h_out + (int64_t)gq * a.ldh + col;
-              *(uint2*)hrow = make_uint2(pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3]));
-              *(uint2*)(hrow + a.hidden) = make_uint2(pack_bf16x2(uv[0], uv[1]), pack_bf16x2(uv[2], uv[3]));
+            if (row_ok) {
+              bf16_t* orow = a.out + (int64_t)gq * a.ldo + col;
+              *(uint2*)orow = make_uint2(pack_bf16x2(av[0], av[1]), pack_bf16x2(av[2], av[3]));
+              if (a.h_out) {
+                bf16_t* hrow = a.h_out + (int64_t)gq * a.ldh + col;
+                *(uint2*)hrow = make_uint2(pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3]));
+                *(uint2*)(hrow + a.hidden) = make_uint2(pack_bf16x2(uv[0], uv[1]), pack_bf16x2(uv[2], uv[3]));
+              }
             }
           }
-        }
+        };
+        if (a.limit == a.limit)
+          swiglu_rows(std::true_type{});
+        else
+          swiglu_rows(std::false_type{});
       } else if (pt * TP + 64 * wp < a.n_p) {  // wave-uniform: this quarter holds rows of N
         float scl = 1.f;
         int orow_idx = gq;

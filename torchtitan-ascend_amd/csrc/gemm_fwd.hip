@@ -601,40 +601,48 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
       const int gq = row0 + 64 * j + 32 * wq + er32;
       const bool row_ok = gq < row1;
       if constexpr (EPI == EPI_SWIGLU) {
-        const bool clamp = (a.limit == a.limit);
         const float L = a.limit;
-        if (pt * 128 + (128 / WPN) * wp < a.n_p) {
+        // The clamp (swiglu_limit) is wave-uniform: one code path each, so
+        // that the unclamped SwiGLU carries no min / max / select per value.
+        auto swiglu_rows = [&](auto clampc) {
+          constexpr bool CLAMP = decltype(clampc)::value;
 #pragma unroll
-          for (int pb = 0; pb < NPB / 2; ++pb) {
+            for (int pb = 0; pb < NPB / 2; ++pb) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              const int col = pt * 128 + (128 / WPN) * wp + 32 * pb + 8 * g + 4 * half;
-              float av[4], gv[4], uv[4];
+              for (int g = 0; g < 4; ++g) {
+                const int col = pt * 128 + (128 / WPN) * wp + 32 * pb + 8 * g + 4 * half;
+                float av[4], gv[4], uv[4];
 #pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                // h is materialised in bf16 by the reference; SwiGLU reads it.
-                gv[i] = round_bf16(acc[pb][j][4 * g + i]);
-                uv[i] = round_bf16(acc[pb + NPB / 2][j][4 * g + i]);
-                float gc = gv[i], uc = uv[i];
-                if (clamp) {
-                  gc = fminf(gc, L);
-                  uc = fminf(fmaxf(uc, -L), L);
+                for (int i = 0; i < 4; ++i) {
+                  // h is materialised in bf16 by the reference; SwiGLU reads it.
+                  gv[i] = round_bf16(acc[pb][j][4 * g + i]);
+                  uv[i] = round_bf16(acc[pb + NPB / 2][j][4 * g + i]);
+                  float gc = gv[i], uc = uv[i];
+                  if constexpr (CLAMP) {
+                    gc = fminf(gc, L);
+                    uc = fminf(fmaxf(uc, -L), L);
+                  }
+                  av[i] = silu_f(gc) * uc;
                 }
-                av[i] = silu_f(gc) * uc;
-              }
-              if (row_ok) {
-                bf16_t* orow = a.out + (int64_t)gq * a.ldo + col;
-                *(uint2*)orow = make_uint2(pack_bf16x2(av[0], av[1]), pack_bf16x2(av[2], av[3]));
-                if (a.h_out) {
-                  bf16_t* hrow = a.h_out + (int64_t)gq * a.ldh + col;
-                  *(uint2*)hrow = make_uint2(pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3]));
-                  *(uint2*)(hrow + a.hidden) =
-                      make_uint2(pack_bf16x2(uv[0], uv[1]), pack_bf16x2(uv[2], uv[3]));
+                if (row_ok) {
+                  bf16_t* orow = a.out + (int64_t)gq * a.ldo + col;
+                  *(uint2*)orow = make_uint2(pack_bf16x2(av[0], av[1]), pack_bf16x2(av[2], av[3]));
+                  if (a.h_out) {
+                    bf16_t* hrow = a.h_out + (int64_t)gq * a.ldh + col;
+                    *(uint2*)hrow = make_uint2(pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3]));
+                    *(uint2*)(hrow + a.hidden) =
+                        make_uint2(pack_bf16x2(uv[0], uv[1]), pack_bf16x2(uv[2], uv[3]));
+                  }
                 }
               }
+              __builtin_amdgcn_sched_barrier(0);
             }
-            __builtin_amdgcn_sched_barrier(0);
-          }
+        };
+        if (pt * 128 + (128 / WPN) * wp < a.n_p) {
+          if (a.limit == a.limit)
+            swiglu_rows(std::true_type{});
+          else
+            swiglu_rows(std::false_type{});
         }
       } else if constexpr (EPI == EPI_SWIGLU_BWD) {
         // acc = dA = g for output columns p of the activation; with the saved
