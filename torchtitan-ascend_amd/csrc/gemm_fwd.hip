@@ -604,39 +604,52 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
         const float L = a.limit;
         // The clamp (swiglu_limit) is wave-uniform: one code path each, so
         // that the unclamped SwiGLU carries no min / max / select per value.
+        // Per 32-column block: gate and up are rounded to bf16 two at a time
+        // (one two-wide conversion each; the bf16 pairs are what h_out
+        // stores), then the row's stores share one address and one branch.
         auto swiglu_rows = [&](auto clampc) {
           constexpr bool CLAMP = decltype(clampc)::value;
 #pragma unroll
-            for (int pb = 0; pb < NPB / 2; ++pb) {
+          for (int pb = 0; pb < NPB / 2; ++pb) {
+            uint32_t ap[4][2], gp[4][2], up[4][2];
 #pragma unroll
-              for (int g = 0; g < 4; ++g) {
-                const int col = pt * 128 + (128 / WPN) * wp + 32 * pb + 8 * g + 4 * half;
-                float av[4], gv[4], uv[4];
+            for (int g = 0; g < 4; ++g) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                  // h is materialised in bf16 by the reference; SwiGLU reads it.
-                  gv[i] = round_bf16(acc[pb][j][4 * g + i]);
-                  uv[i] = round_bf16(acc[pb + NPB / 2][j][4 * g + i]);
-                  float gc = gv[i], uc = uv[i];
+              for (int i2 = 0; i2 < 2; ++i2) {
+                // h is materialised in bf16 by the reference; SwiGLU reads it.
+                const int v = 4 * g + 2 * i2;
+                gp[g][i2] = pack_bf16x2(acc[pb][j][v], acc[pb][j][v + 1]);
+                up[g][i2] = pack_bf16x2(acc[pb + NPB / 2][j][v], acc[pb + NPB / 2][j][v + 1]);
+                float av[2];
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2) {
+                  float gc = __uint_as_float(h2 ? (gp[g][i2] & 0xffff0000u) : (gp[g][i2] << 16));
+                  float uc = __uint_as_float(h2 ? (up[g][i2] & 0xffff0000u) : (up[g][i2] << 16));
                   if constexpr (CLAMP) {
                     gc = fminf(gc, L);
                     uc = fminf(fmaxf(uc, -L), L);
                   }
-                  av[i] = silu_f(gc) * uc;
+                  av[h2] = silu_f(gc) * uc;
                 }
-                if (row_ok) {
-                  bf16_t* orow = a.out + (int64_t)gq * a.ldo + col;
-                  *(uint2*)orow = make_uint2(pack_bf16x2(av[0], av[1]), pack_bf16x2(av[2], av[3]));
-                  if (a.h_out) {
-                    bf16_t* hrow = a.h_out + (int64_t)gq * a.ldh + col;
-                    *(uint2*)hrow = make_uint2(pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3]));
-                    *(uint2*)(hrow + a.hidden) =
-                        make_uint2(pack_bf16x2(uv[0], uv[1]), pack_bf16x2(uv[2], uv[3]));
-                  }
+                ap[g][i2] = pack_bf16x2(av[0], av[1]);
+              }
+            }
+            if (row_ok) {
+              const int col = pt * 128 + (128 / WPN) * wp + 32 * pb + 4 * half;
+              bf16_t* orow = a.out + (int64_t)gq * a.ldo + col;
+#pragma unroll
+              for (int g = 0; g < 4; ++g) *(uint2*)(orow + 8 * g) = make_uint2(ap[g][0], ap[g][1]);
+              if (a.h_out) {
+                bf16_t* hrow = a.h_out + (int64_t)gq * a.ldh + col;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                  *(uint2*)(hrow + 8 * g) = make_uint2(gp[g][0], gp[g][1]);
+                  *(uint2*)(hrow + a.hidden + 8 * g) = make_uint2(up[g][0], up[g][1]);
                 }
               }
-              __builtin_amdgcn_sched_barrier(0);
             }
+            __builtin_amdgcn_sched_barrier(0);
+          }
         };
         if (pt * 128 + (128 / WPN) * wp < a.n_p) {
           if (a.limit == a.limit)
