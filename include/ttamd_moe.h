@@ -352,7 +352,8 @@ int ttamd_grouped_mm(const void* x, const void* w, const int32_t* offs,
 /*
  * Fused expert up-projection: h = x @ w13[e]^T (w13 [E, 2H, D], rows 0..H-1
  * gate, H..2H-1 up), optional clamp (gate <= L, -L <= up <= L with
- * L = swiglu_limit, applied for every L >= 0, including 0), a = silu(gate) * up.
+ * L = swiglu_limit, applied for every L >= 0, including 0; as torch.clamp, a
+ * NaN stays NaN), a = silu(gate) * up.
  * Replaces npu_gmm.py:29-37 (cumsum, grouped_mm w13, clamp, npu_swiglu).
  * x [M, D] -> a [M, H] bf16; h_out (nullable) receives the unclamped
  * pre-activation bf16 [M, 2H] for the backward.  H % 64 == 0, D % 64 == 0.
@@ -483,9 +484,11 @@ int ttamd_grouped_mm_dgrad(const void* dy, const void* w, const int32_t* offs,
  * Grouped dgrad of the down projection fused with the SwiGLU backward:
  *   g[m, p]  = sum_d dy[m, d] * w2[e(m), d, p]          (dA, fp32)
  *   with h = [gate | up] from ttamd_grouped_mm_swiglu (h_out), L = limit:
- *   gc = min(gate, L), uc = clamp(up, -L, L)   (identity when L <= 0)
- *   dgate = g * uc * silu'(gc) * [gate <= L]
- *   dup   = g * silu(gc)       * [-L <= up <= L]
+ *   gc = min(gate, L), uc = clamp(up, -L, L)   (NaN stays NaN)
+ *   dgate = [gate <= L]      ? g * uc * silu'(gc) : 0
+ *   dup   = [-L <= up <= L]  ? g * silu(gc)       : 0
+ *   (torch.clamp's backward: exactly 0 where it clamps or meets a NaN;
+ *   without a clamp every mask is true)
  *   dh[m] = [dgate | dup]  bf16 [M, 2H]
  * a_out (nullable) receives silu(gc)*uc recomputed in bf16 [M, H].
  * D % 64 == 0, H % 128 == 0; swiglu_limit NaN = no clamp.

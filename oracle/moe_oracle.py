@@ -42,7 +42,9 @@ PINNED = {
                        "of router_forward_f64 (a dropped renorm term or a wrong softmax Jacobian fails them)",
     "grouped_dgrad / grouped_wgrad": "through moe_backward's autograd golden (they are its dx / dW steps); "
                                      "brute-force triple loop on tiny shapes",
-    "swiglu_backward": "through moe_backward (above); finite differences of swiglu on clamped and unclamped values",
+    "swiglu_backward": "through moe_backward (above); finite differences of swiglu on clamped and unclamped "
+                       "values; torch CPU autograd of torch.clamp + silu * up on NaN, +-inf, the limit and "
+                       "signed zeros",
     "expert_weight_grad_slices": "equal to the matching slices of moe_backward's full dw13 / dw2 on small shapes "
                                  "(a swapped gate/up half or a transposed slice fails it)",
     "bf16_round": "torch .to(bfloat16) on random and special values",
@@ -289,7 +291,8 @@ def router_forward_f64(x: np.ndarray, w_router: np.ndarray, idx: np.ndarray, sco
 # ---------------------------------------------------------------------------
 def silu(x: np.ndarray) -> np.ndarray:
     x = np.asarray(x, np.float64)
-    return (x / (1.0 + np.exp(-x))).astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):  # silu(-inf) is NaN, as in torch
+        return (x / (1.0 + np.exp(-x))).astype(np.float32)
 
 
 def grouped_mm(x: np.ndarray, w: np.ndarray, offs: np.ndarray) -> np.ndarray:
@@ -471,23 +474,26 @@ def moe_backward(x, top_scores, idx, w13, w2, num_experts, score_before_experts,
 
 def swiglu_backward(da: np.ndarray, h: np.ndarray, swiglu_limit: float | None = None) -> np.ndarray:
     """Gradient of swiglu(clamp(h)) (npu_gmm.py:32-37) w.r.t. the
-    pre-activation h = [gate | up], given da = d(activation): the clamp masks
-    come from h itself (torch.clamp's gradient is zero where it clamps).
-    Returns dh [.., 2H] = [da * up_c * silu'(gate_c) * [gate <= L],
-    da * silu(gate_c) * [-L <= up <= L]]."""
+    pre-activation h = [gate | up], given da = d(activation).  torch.clamp's
+    backward is where(min <= h <= max, grad, 0): exactly zero where it
+    clamped and where h is NaN, whatever the incoming gradient holds.
+    Returns dh [.., 2H] = [[gate <= L] ? da * up_c * silu'(gate_c) : 0,
+    [-L <= up <= L] ? da * silu(gate_c) : 0]."""
     H = h.shape[-1] // 2
     gate, up = h[..., :H], h[..., H:]
     gc, uc = gate, up
-    mg = np.ones_like(gate)
-    mu = np.ones_like(up)
     if swiglu_limit is not None:
-        mg = (gate <= swiglu_limit).astype(np.float32)
-        mu = ((up >= -swiglu_limit) & (up <= swiglu_limit)).astype(np.float32)
         gc = np.minimum(gate, swiglu_limit)
         uc = np.clip(up, -swiglu_limit, swiglu_limit)
-    sig = (1.0 / (1.0 + np.exp(-gc.astype(np.float64)))).astype(np.float32)
-    dsilu = sig * (1.0 + gc * (1.0 - sig))
-    return np.concatenate([da * uc * dsilu * mg, da * gc * sig * mu], axis=-1).astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        sig = (1.0 / (1.0 + np.exp(-gc.astype(np.float64)))).astype(np.float32)
+        dsilu = sig * (1.0 + gc * (1.0 - sig))
+        dgate = da * uc * dsilu
+        dup = da * gc * sig
+        if swiglu_limit is not None:
+            dgate = np.where(gate <= swiglu_limit, dgate, np.float32(0))
+            dup = np.where((up >= -swiglu_limit) & (up <= swiglu_limit), dup, np.float32(0))
+    return np.concatenate([dgate, dup], axis=-1).astype(np.float32)
 
 
 def expert_weight_grad_slices(routed: np.ndarray, dy: np.ndarray, w13_e: np.ndarray, w2_e: np.ndarray,

@@ -240,6 +240,44 @@ def test_swiglu_backward_finite_differences():
             assert abs(fd - dh[r, c]) < 1e-3 * max(1.0, abs(fd)), (limit, r, c)
 
 
+def test_swiglu_clamp_special_values_match_torch_autograd():
+    """NaN, +-inf, values on the limit and signed zeros through the
+    reference's op sequence (npu_gmm.py:32-37: torch.clamp of up and gate,
+    then silu(gate) * up) under torch autograd on the CPU, against the
+    oracle's forward and backward: torch.clamp keeps NaN in its forward and
+    its backward is where(in range, grad, 0)."""
+    import math
+
+    import torch
+    import torch.nn.functional as F
+
+    L = 0.5
+    vals = [math.nan, math.inf, -math.inf, L, -L, 0.0, -0.0, 0.3, -0.3, 2.0, -2.0]
+    pairs = [(g, u) for g in vals for u in vals]
+    h = np.array(pairs, np.float32)  # [n, 2]: H = 1, gate then up
+    da = np.random.default_rng(24).standard_normal((len(pairs), 1)).astype(np.float32)
+
+    hh = torch.tensor(h, requires_grad=True)
+    gate, up = hh.chunk(2, -1)
+    up = torch.clamp(up, min=-L, max=L)
+    gate = torch.clamp(gate, max=L)
+    a = F.silu(gate) * up
+    a.backward(torch.tensor(da))
+    want_a = a.detach().numpy()
+    want_dh = hh.grad.numpy()
+
+    got_a = O.swiglu(h, L)
+    got_dh = O.swiglu_backward(da, h, L)
+    for got, want, what in ((got_a, want_a, "forward"), (got_dh, want_dh, "backward")):
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(want), err_msg=f"{what}: NaN positions")
+        fin = ~np.isnan(want)
+        np.testing.assert_allclose(got[fin], want[fin], rtol=1e-6, atol=1e-7, err_msg=what)
+    # the clamp's gradient is exactly zero where it clamps or meets NaN
+    g_out = (h[:, 0] > L) | np.isnan(h[:, 0])
+    u_out = (np.abs(h[:, 1]) > L) | np.isnan(h[:, 1])
+    assert (got_dh[g_out, 0] == 0).all() and (got_dh[u_out, 1] == 0).all()
+
+
 def test_dscores_abs_bounds_dscores():
     """The dot-product scale returned with dscores bounds it: |<a,b>| <= sum|a b|."""
     rng = np.random.default_rng(23)

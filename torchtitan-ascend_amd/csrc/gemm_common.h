@@ -19,6 +19,14 @@ enum Epi {
 __device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 __device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 
+// torch.clamp(x, max=L) and torch.clamp(x, -L, L): NaN stays NaN (the IEEE
+// 754-2019 minimum / maximum, v_minimum3_f32 / v_maximum3_f32 on gfx950),
+// where fminf / fmaxf would return the limit.
+__device__ __forceinline__ float clamp_max_nan(float x, float L) { return __builtin_elementwise_minimum(x, L); }
+__device__ __forceinline__ float clamp_nan(float x, float L) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_minimum(x, L), -L);
+}
+
 // Token-row tiles: table[i] = {expert, first row, end row, 0}, at most
 // kFwdTileRows rows (bf16 forward and dgrad) or kFp8TileRows (fp8).  The
 // workspace is sized for tiles of kTileRows rows, fewer rows than either,

@@ -350,8 +350,8 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fp8_kernel(const Fp8Args a) {
               uv[i] = round_bf16(acc[pb + 2][jb][i]);
               float gc = gv[i], uc = uv[i];
               if constexpr (CLAMP) {
-                gc = fminf(gc, L);
-                uc = fminf(fmaxf(uc, -L), L);
+                gc = clamp_max_nan(gc, L);
+                uc = clamp_nan(uc, L);
               }
               av[i] = silu_f(gc) * uc;
             }

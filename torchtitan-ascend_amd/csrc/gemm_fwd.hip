@@ -490,7 +490,11 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
       gint_t* const split_cnt = (gint_t*)(((uint64_t)(uint32_t)pc.w << 32) | (uint32_t)pc.z);
       uint64_t pw = (uint64_t)part + (uint64_t)pc_t * np * kSplitPartBytes + (uint64_t)w * np * (NPB * NJ * BLK);
       asm volatile("" : "+s"(pw));
-      uint32_t loff = (uint32_t)l * 16u;
+      // the lane id re-derived here (mbcnt of an opaque zero, which the
+      // compiler cannot hoist), not kept through the k loop
+      uint32_t zero = 0;
+      asm volatile("" : "+v"(zero));
+      uint32_t loff = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, zero)) * 16u;
       asm volatile("" : "+v"(loff));
       const uint32_t bstride = (uint32_t)np * BLK;  // one block of every piece
 #pragma unroll
@@ -626,8 +630,8 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
                   float gc = __uint_as_float(h2 ? (gp[g][i2] & 0xffff0000u) : (gp[g][i2] << 16));
                   float uc = __uint_as_float(h2 ? (up[g][i2] & 0xffff0000u) : (up[g][i2] << 16));
                   if constexpr (CLAMP) {
-                    gc = fminf(gc, L);
-                    uc = fminf(fmaxf(uc, -L), L);
+                    gc = clamp_max_nan(gc, L);
+                    uc = clamp_nan(uc, L);
                   }
                   av[h2] = silu_f(gc) * uc;
                 }
@@ -662,17 +666,21 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
         // bf16 pre-activation h = [gate | up]: dgate, dup (clamp masks from
         // the bf16 h, as the reference's autograd sees them).  The 8 h values
         // of a 32-column block are loaded before any is used.
-        const bool clamp = (a.limit == a.limit);
-        const float L = a.limit;
+        // Without a clamp the limit is +inf: minimum / maximum against it are
+        // exact no-ops (NaN included) and the masks are forced true, so the
+        // value loop has no branch on the clamp.
+        const bool noclamp = !(a.limit == a.limit);
+        const float L = noclamp ? __builtin_inff() : a.limit;
 #pragma unroll
         for (int pb = 0; pb < NPB; ++pb) {
           const int blk = j * NPB + pb;
           if (blk + 1 < NJV * NPB) load_h((blk + 1) / NPB, (blk + 1) % NPB, hbuf[(blk + 1) & 1]);
           const uint2 (&hv)[4][2] = hbuf[blk & 1];
           if (pt * TP + arow[pb] < a.n_p && row_ok) {
+            const int col0 = pt * TP + arow[pb] + 4 * half;
+            bf16_t* drow = a.out + (int64_t)gq * a.ldo + col0;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-              const int col = pt * TP + arow[pb] + 8 * g + 4 * half;
               const uint2 hg = hv[g][0];
               const uint2 hu = hv[g][1];
               const float gate[4] = {bf16_to_f32(hg.x & 0xffff), bf16_to_f32(hg.x >> 16),
@@ -684,26 +692,27 @@ __global__ __launch_bounds__(FTHREADS, 1) void gg_fwd_kernel(const FwdArgs a) {
               for (int i = 0; i < 4; ++i) {
                 const float gd = acc[pb][j][4 * g + i];
                 float gc = gate[i], uc = up[i];
-                float mg = 1.f, mu = 1.f;
-                if (clamp) {
-                  if (gc > L) { gc = L; mg = 0.f; }
-                  if (uc > L) { uc = L; mu = 0.f; }
-                  if (uc < -L) { uc = -L; mu = 0.f; }
-                }
+                // torch.clamp's backward: where(in range, grad, 0), so exactly
+                // zero where it clamped and where h is NaN
+                const bool kg = noclamp | (gc <= L);
+                const bool ku = noclamp | ((uc >= -L) & (uc <= L));
+                gc = clamp_max_nan(gc, L);
+                uc = clamp_nan(uc, L);
                 const float sig = sigmoid_f(gc);
                 const float sv = gc * sig;
                 const float ds = sig * (1.f + gc * (1.f - sig));
-                dg[i] = gd * uc * ds * mg;
-                du[i] = gd * sv * mu;
+                dg[i] = kg ? gd * uc * ds : 0.f;
+                du[i] = ku ? gd * sv : 0.f;
                 av[i] = sv * uc;
               }
-              bf16_t* drow = a.out + (int64_t)gq * a.ldo + col;
-              *(uint2*)drow = make_uint2(pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3]));
-              *(uint2*)(drow + a.hidden) = make_uint2(pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3]));
+              *(uint2*)(drow + 8 * g) = make_uint2(pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3]));
+              *(uint2*)(drow + a.hidden + 8 * g) =
+                  make_uint2(pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3]));
               if (a.a_out) {
-                bf16_t* arow_p = a.a_out + (int64_t)gq * a.hidden + col;
+                bf16_t* arow_p = a.a_out + (int64_t)gq * a.hidden + col0 + 8 * g;
                 *(uint2*)arow_p = make_uint2(pack_bf16x2(av[0], av[1]), pack_bf16x2(av[2], av[3]));
               }
+              __builtin_amdgcn_sched_barrier(0);
             }
           }
           __builtin_amdgcn_sched_barrier(0);
