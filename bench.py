@@ -444,6 +444,9 @@ def main():
             "traffic": measured_traffic(args.config),
             "algorithmic_flops_per_launch": w13_flops,
             "avg_launch_us": round(kernel_us, 2),
+            # the same launch against the HBM bound (the C2 w13 sits near the
+            # MI355X ridge): its algorithmic bytes over its launch time
+            "hbm_view": w13_hbm_view(cfg, fp8, T, M, kernel_us, measured_traffic(args.config)),
         },
     }
 
@@ -452,6 +455,28 @@ def main():
                                               zipf_scores if zipf_idx is not None else None,
                                               (sw13, sw2) if shared else None)
     print(json.dumps(result), flush=True)
+
+
+def w13_hbm_view(cfg, fp8, T, M, kernel_us, traffic):
+    """Algorithmic HBM bytes of one w13 launch and their rate: the token rows
+    read once (x [T, D] when the gather is fused into the loads, the routed
+    rows [M, D] otherwise; e4m3 plus per-128-channel scales for fp8), the
+    weights [E, 2H, D] once (with their 128 x 128 block scales for fp8), the
+    activation a [M, H] written (and the pre-activation h [M, 2H] when the
+    training step saves it), and 4-byte row ids for the fused gather."""
+    D, H, E = cfg["D"], cfg["H"], cfg["E"]
+    if fp8:
+        nbytes = M * D + M * (D // 128) * 4 + E * 2 * H * D + E * (2 * H // 128) * (D // 128) * 4 + M * H * 2
+    else:
+        gather = not (cfg["score_before"] or D < 128 or cfg["backward"])
+        nbytes = ((T if gather else M) * D * 2 + E * 2 * H * D * 2 + M * H * 2
+                  + (M * 2 * H * 2 if cfg["backward"] else 0) + (4 * M if gather else 0))
+    gbs = nbytes / (kernel_us * 1e-6) / 1e9
+    view = {"algorithmic_bytes": nbytes, "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    if traffic:
+        view["measured_traffic_gbs"] = round(traffic / (kernel_us * 1e-6) / 1e9, 1)
+    return view
 
 
 def roofline_kernel_name(cfg, fp8):
